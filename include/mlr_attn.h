@@ -1,0 +1,181 @@
+/*
+ * mlr_attn.h - C ABI of the MI355X paged-attention library (libmlr_attn.so).
+ *
+ * The library implements the three kernels of the paged attention path of
+ * mini-llm-runtime on gfx950 (MI355X):
+ *   1. the KV-cache write: a slot_mapping scatter into one layer's block pool;
+ *   2. batched single-token paged decode (split-KV, two passes);
+ *   3. paged chunk-prefill attention (causal by absolute token position).
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers, except where a comment says otherwise.
+ *   - A KV cache layer is one contiguous array of shape
+ *     [num_blocks, block_size, num_kv_heads, head_dim]; slot s addresses the
+ *     row [s / block_size, s % block_size]. This is the per-layer view that
+ *     PagedKVCache.get_layer_cache hands out (runtime/paged_kv_cache.py:25-35,
+ *     251-259 in the reference).
+ *   - Strides are in elements, not bytes. Query and output rows are unit-stride
+ *     along head_dim; the KV-write sources may have any strides.
+ *   - Query head h reads KV head h / (num_q_heads / num_kv_heads) (GQA).
+ *   - Calls are asynchronous on `stream` (a hipStream_t); none synchronises the
+ *     host and none allocates device memory. Outputs and workspaces are owned
+ *     by the caller.
+ *   - Return value: MLR_OK (0) or an mlr_status code; mlr_last_error() then
+ *     holds a message for the calling thread. Argument errors are detected
+ *     before any kernel is launched, so a failed call leaves memory untouched.
+ *   - Metadata contents (slot values, block ids, lengths) are validated by the
+ *     host layer before the call. Kernels still never access memory outside the
+ *     buffers described by the size arguments: an out-of-range slot is skipped
+ *     and an out-of-range block id masks its tokens.
+ */
+#ifndef MLR_ATTN_H
+#define MLR_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. Values match nothing in torch; the host layer maps them. */
+enum mlr_dtype {
+  MLR_DTYPE_F32 = 0,
+  MLR_DTYPE_F16 = 1,
+  MLR_DTYPE_BF16 = 2,
+  MLR_DTYPE_F64 = 3
+};
+
+/* Index element types for slot_mapping. */
+enum mlr_index_dtype { MLR_INDEX_I32 = 0, MLR_INDEX_I64 = 1 };
+
+enum mlr_status {
+  MLR_OK = 0,
+  MLR_ERR_INVALID = 1,     /* bad argument (shape, stride, pointer, size)  */
+  MLR_ERR_UNSUPPORTED = 2, /* valid, but outside what the kernels cover     */
+  MLR_ERR_WORKSPACE = 3,   /* workspace missing or too small                */
+  MLR_ERR_HIP = 4          /* the HIP runtime reported an error at launch   */
+};
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char *mlr_last_error(void);
+
+/* Library ABI version (major * 10000 + minor * 100 + patch). */
+int mlr_version(void);
+
+/*
+ * KV-cache write: k_cache[slot_mapping[t]] = convert(k[t]) and the same for v,
+ * for t in [0, num_tokens). Conversion between element types rounds to
+ * nearest-even, as Tensor.to does; equal types copy bits.
+ *
+ * Replaces PagedKVCache.write_slots (runtime/paged_kv_cache.py:194-249), the
+ * two index_copy_ calls at :243-249. Slots must be distinct (the host layer
+ * rejects duplicates, :238-239); slots outside [0, num_slots) are skipped.
+ *   k, v           : [num_tokens, num_kv_heads, head_dim] in src_dtype, any
+ *                    strides (the host layer may pass transposed views)
+ *   slot_mapping   : [num_tokens], index_dtype
+ *   k_cache,v_cache: one layer, [num_slots / block_size, block_size,
+ *                    num_kv_heads, head_dim] contiguous, cache_dtype
+ */
+int mlr_kv_write(const void *k, const void *v, int src_dtype,
+                 int64_t num_tokens, int64_t k_stride_t, int64_t k_stride_h,
+                 int64_t k_stride_d, int64_t v_stride_t, int64_t v_stride_h,
+                 int64_t v_stride_d,
+                 const void *slot_mapping, int index_dtype, void *k_cache,
+                 void *v_cache, int cache_dtype, int64_t num_slots,
+                 int64_t num_kv_heads, int64_t head_dim, void *stream);
+
+/*
+ * Bytes of workspace mlr_paged_decode needs for these sizes. `max_context`
+ * bounds every context length (the host passes block_table width * block_size).
+ * tokens_per_split <= 0 selects the library's default split size.
+ */
+size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
+                                       int64_t head_dim, int64_t max_context,
+                                       int64_t tokens_per_split, int dtype);
+
+/*
+ * Batched single-token paged decode:
+ *   out[b, h] = softmax_t(scale * q[b, h] . K[b, t, h/G]) @ V[b, t, h/G]
+ * over t < context_lens[b], where token t of sequence b lives in physical block
+ * block_tables[b, t / block_size] at offset t % block_size.
+ *
+ * Replaces paged_attention_decode_batch_parallel
+ * (kernels/reference/paged_attention.py:178-254) and, with batch = 1, the
+ * single-request paged_attention_decode (:6-105). Softmax statistics and the
+ * split combine are FP32 (FP64 inputs keep FP64 dot products and P@V).
+ *   q            : [batch, num_q_heads, head_dim], strides (q_stride_b, q_stride_h)
+ *   block_tables : int64 [batch, >= max_blocks_per_seq], row stride
+ *                  block_table_stride; entries past ceil(ctx/block_size) unused
+ *   context_lens : int64 [batch]; each in [1, max_blocks_per_seq * block_size]
+ *   tokens_per_split: split-KV granularity in tokens (<= 0: library default)
+ *   workspace    : >= mlr_paged_decode_workspace_size(...) bytes, 256-aligned
+ *   out          : [batch, num_q_heads, head_dim], strides (out_stride_b, out_stride_h)
+ */
+int mlr_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void *k_cache, const void *v_cache,
+                     int64_t num_blocks, int64_t block_size,
+                     int64_t num_kv_heads, int64_t head_dim,
+                     const int64_t *block_tables, int64_t block_table_stride,
+                     int64_t max_blocks_per_seq, const int64_t *context_lens,
+                     int64_t batch, int64_t num_q_heads, double scale,
+                     int dtype, int64_t tokens_per_split, void *workspace,
+                     size_t workspace_bytes, void *out, int64_t out_stride_b,
+                     int64_t out_stride_h, void *stream);
+
+/*
+ * Paged chunk-prefill attention for a packed batch of sequences (varlen):
+ * sequence s owns query rows [query_start_loc[s], query_start_loc[s+1]) of q,
+ * whose absolute positions are prefix_len_s + i with
+ * prefix_len_s = context_lens[s] - query_len_s. Query i of sequence s attends to
+ * every cached key at position p <= prefix_len_s + i (the chunk's own keys must
+ * already be written to the cache).
+ *
+ * Replaces paged_attention_prefill_chunk_tiled
+ * (kernels/reference/paged_attention.py:346-434): FP32 online softmax and FP32
+ * P@V, output rounded once to the input type. kv_tile selects the key tile the
+ * kernel steps by (16, 64 or 128; other values pick the nearest supported).
+ *   q               : [total_q, num_q_heads, head_dim], strides (q_stride_t, q_stride_h)
+ *   block_tables    : int64 [num_seqs, >= max_blocks_per_seq], row stride
+ *   query_start_loc : int64 [num_seqs + 1], non-decreasing, starts at 0
+ *   context_lens    : int64 [num_seqs]; context >= query_len,
+ *                     context <= max_blocks_per_seq * block_size
+ *   max_query_len   : upper bound of every query_len (sizes the grid)
+ *   out             : [total_q, num_q_heads, head_dim], strides (out_stride_t, out_stride_h)
+ */
+int mlr_paged_prefill(const void *q, int64_t q_stride_t, int64_t q_stride_h,
+                      const void *k_cache, const void *v_cache,
+                      int64_t num_blocks, int64_t block_size,
+                      int64_t num_kv_heads, int64_t head_dim,
+                      const int64_t *block_tables, int64_t block_table_stride,
+                      int64_t max_blocks_per_seq,
+                      const int64_t *query_start_loc,
+                      const int64_t *context_lens, int64_t num_seqs,
+                      int64_t max_query_len, int64_t num_q_heads, double scale,
+                      int dtype, int64_t kv_tile, void *out,
+                      int64_t out_stride_t, int64_t out_stride_h, void *stream);
+
+/*
+ * Single-sequence chunk prefill with host-side scalars, the exact argument
+ * shape of paged_attention_prefill_chunk_tiled(q, k_cache, v_cache,
+ * block_table, prefix_len, context_len, block_size, tile_size)
+ * (kernels/reference/paged_attention.py:346-356). block_table is an int64
+ * device array of at least ceil(context_len / block_size) entries and
+ * context_len == prefix_len + chunk_len.
+ */
+int mlr_paged_prefill_chunk(const void *q, int64_t q_stride_t,
+                            int64_t q_stride_h, const void *k_cache,
+                            const void *v_cache, int64_t num_blocks,
+                            int64_t block_size, int64_t num_kv_heads,
+                            int64_t head_dim, const int64_t *block_table,
+                            int64_t block_table_len, int64_t prefix_len,
+                            int64_t context_len, int64_t num_q_heads,
+                            double scale, int dtype, int64_t kv_tile,
+                            void *out, int64_t out_stride_t,
+                            int64_t out_stride_h, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLR_ATTN_H */

@@ -1,0 +1,52 @@
+// Declarations shared by the decode translation units.
+#pragma once
+
+#include "mlr_common.h"
+
+namespace mlr {
+
+// Everything a decode kernel needs; built once by mlr_paged_decode.
+struct DecodeParams {
+  const void *q;
+  int64_t q_sb, q_sh;
+  const void *kc;
+  const void *vc;
+  int64_t num_blocks;
+  int64_t block_size;
+  int hkv;
+  int d;
+  const int64_t *bt;
+  int64_t bt_stride;
+  int64_t max_blocks;
+  const int64_t *ctx;
+  int batch;
+  int hq;
+  int group;
+  double scale;
+  int ts;          // tokens per split
+  int max_splits;  // splits covering max_blocks * block_size tokens
+  float2 *ws_ml;   // [batch][hq][max_splits] = (m in natural-log units, l)
+  void *ws_acc;    // [batch][hq][max_splits][d], FP32 (FP64 for f64 inputs)
+  void *out;
+  int64_t o_sb, o_sh;
+};
+
+struct DecodeWorkspace {
+  int64_t ml_bytes;
+  int64_t acc_offset;
+  int64_t total;
+};
+
+int64_t default_tokens_per_split(int dtype, int64_t head_dim);
+DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
+                                        int64_t max_splits, int dtype);
+
+// bf16, head_dim 64/128, GQA group <= 16 and block_size a multiple of 16.
+bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
+                          int64_t block_size);
+int launch_decode_mfma(const DecodeParams &p, hipStream_t stream);
+
+template <typename T>
+int launch_combine(const DecodeParams &p, hipStream_t stream);
+
+}  // namespace mlr

@@ -1,0 +1,354 @@
+// Batched single-token paged decode, split-KV in two passes.
+//
+// Pass 1 (split kernel): one workgroup per (sequence, KV head, split of
+// tokens_per_split tokens) computes, for every query head of the KV head's
+// GQA group, the split-local softmax statistics m = max_t s_t,
+// l = sum_t exp(s_t - m) and acc = sum_t exp(s_t - m) v_t, and stores them in
+// the FP32 workspace. Pass 2 (combine kernel) merges the splits of one
+// (sequence, query head) with the log-sum-exp rule
+//   M = max_s m_s,  out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.
+//
+// Math follows paged_attention_decode_batch_parallel
+// (kernels/reference/paged_attention.py:178-254): scores are q.k in the input
+// type (the reference's matmul rounds them to the input type), multiplied by
+// scale (rounded again), then an FP32 softmax over positions t < seq_len;
+// positions past seq_len and padded block-table entries never contribute.
+//
+// bf16 inputs with head_dim 64 or 128 and at most 16 query heads per KV head
+// take the MFMA kernel in paged_decode_mfma.hip; everything else takes the
+// generic kernel below.
+#include "mlr_common.h"
+#include "paged_decode.h"
+
+namespace mlr {
+namespace {
+
+constexpr int kGenHeads = 16;       // query heads handled per generic workgroup
+constexpr int kGenMaxSplit = 512;   // tokens per split the generic kernel holds
+
+// Score as the reference computes it: the matmul output in the element type,
+// times scale in FP32 opmath, rounded to the element type, then FP32.
+template <typename T>
+__device__ __forceinline__ float decode_score(typename Elem<T>::acc dot,
+                                              double scale) {
+  if constexpr (std::is_same<T, double>::value) {
+    return static_cast<float>(dot * scale);
+  } else {
+    const float r = Elem<T>::round_acc(dot);
+    return Elem<T>::round_acc(r * static_cast<float>(scale));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void decode_split_generic(DecodeParams p) {
+  using E = Elem<T>;
+  using Acc = typename E::acc;
+  const int split = blockIdx.x;
+  const int nhc = static_cast<int>(ceil_div(p.group, kGenHeads));
+  const int kvh = blockIdx.y / nhc;
+  const int g0 = (blockIdx.y % nhc) * kGenHeads;
+  const int ng = min(kGenHeads, p.group - g0);
+  const int b = blockIdx.z;
+
+  const int64_t cap = p.max_blocks * p.block_size;
+  int64_t ctx = p.ctx[b];
+  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int64_t t0 = static_cast<int64_t>(split) * p.ts;
+  if (t0 >= ctx) return;
+  const int n = static_cast<int>(min<int64_t>(p.ts, ctx - t0));
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  Acc *q_s = reinterpret_cast<Acc *>(smem);                       // [16][d]
+  int64_t *row_s = reinterpret_cast<int64_t *>(q_s + kGenHeads * p.d);  // [ts]
+  float *s_s = reinterpret_cast<float *>(row_s + p.ts);           // [16][ts]
+
+  const T *q = static_cast<const T *>(p.q);
+  const T *kc = static_cast<const T *>(p.kc);
+  const T *vc = static_cast<const T *>(p.vc);
+  const int head0 = kvh * p.group + g0;
+
+  for (int i = threadIdx.x; i < ng * p.d; i += blockDim.x) {
+    const int g = i / p.d, e = i % p.d;
+    q_s[i] = E::to_acc(q[b * p.q_sb + (head0 + g) * p.q_sh + e]);
+  }
+  // Element offset of each token's K/V row for this KV head, or -1 when the
+  // block-table entry is not a valid block id.
+  for (int t = threadIdx.x; t < n; t += blockDim.x) {
+    const int64_t pos = t0 + t;
+    const int64_t blk = p.bt[b * p.bt_stride + pos / p.block_size];
+    row_s[t] = (blk >= 0 && blk < p.num_blocks)
+                   ? ((blk * p.block_size + pos % p.block_size) * p.hkv + kvh) * p.d
+                   : -1;
+  }
+  __syncthreads();
+
+  for (int i = threadIdx.x; i < n * ng; i += blockDim.x) {
+    const int t = i / ng, g = i % ng;
+    const int64_t r = row_s[t];
+    float s = -INFINITY;
+    if (r >= 0) {
+      Acc dot = 0;
+      const T *kr = kc + r;
+      const Acc *qg = q_s + g * p.d;
+      for (int e = 0; e < p.d; ++e) dot += qg[e] * E::to_acc(kr[e]);
+      s = decode_score<T>(dot, p.scale);
+    }
+    s_s[g * p.ts + t] = s;
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  for (int g = wave; g < ng; g += nw) {
+    float m = -INFINITY;
+    for (int t = lane; t < n; t += kWave) m = fmaxf(m, s_s[g * p.ts + t]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int t = lane; t < n; t += kWave) {
+      const float e = (m == -INFINITY) ? 0.f : expf(s_s[g * p.ts + t] - m);
+      s_s[g * p.ts + t] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      p.ws_ml[((int64_t)b * p.hq + head0 + g) * p.max_splits + split] =
+          make_float2(m, l);
+    }
+  }
+  __syncthreads();
+
+  Acc *ws_acc = static_cast<Acc *>(p.ws_acc);
+  for (int i = threadIdx.x; i < ng * p.d; i += blockDim.x) {
+    const int g = i / p.d, e = i % p.d;
+    Acc a = 0;
+    for (int t = 0; t < n; ++t) {
+      const int64_t r = row_s[t];
+      if (r >= 0) a += static_cast<Acc>(s_s[g * p.ts + t]) * E::to_acc(vc[r + e]);
+    }
+    ws_acc[(((int64_t)b * p.hq + head0 + g) * p.max_splits + split) * p.d + e] = a;
+  }
+}
+
+// Pass 2 for every path: one workgroup per (query head, sequence).
+template <typename T>
+__global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
+  using E = Elem<T>;
+  using Acc = typename E::acc;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int64_t cap = p.max_blocks * p.block_size;
+  int64_t ctx = p.ctx[b];
+  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int ns = static_cast<int>(ceil_div(ctx, p.ts));
+  const float2 *ml = p.ws_ml + ((int64_t)b * p.hq + h) * p.max_splits;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  float *w_s = reinterpret_cast<float *>(smem);  // [max_splits]
+  __shared__ float red[2];
+
+  // Global max, then per-split weights and the total normaliser.
+  float m = -INFINITY;
+  for (int s = threadIdx.x; s < ns; s += blockDim.x) m = fmaxf(m, ml[s].x);
+  m = wave_max(m);
+  __shared__ float wmax[4];
+  if (threadIdx.x % kWave == 0) wmax[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float mm = wmax[0];
+    for (int w = 1; w < (int)(blockDim.x / kWave); ++w) mm = fmaxf(mm, wmax[w]);
+    red[0] = mm;
+  }
+  __syncthreads();
+  const float M = red[0];
+  float l = 0.f;
+  for (int s = threadIdx.x; s < ns; s += blockDim.x) {
+    const float2 v = ml[s];
+    const float w = (v.x == -INFINITY) ? 0.f : expf(v.x - M);
+    w_s[s] = w;
+    l += w * v.y;
+  }
+  l = wave_sum(l);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) wmax[threadIdx.x / kWave] = l;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ll = 0.f;
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) ll += wmax[w];
+    red[1] = ll;
+  }
+  __syncthreads();
+  const float L = red[1];
+
+  const Acc *acc = static_cast<const Acc *>(p.ws_acc) +
+                   ((int64_t)b * p.hq + h) * p.max_splits * p.d;
+  T *out = static_cast<T *>(p.out) + b * p.o_sb + h * p.o_sh;
+  for (int e = threadIdx.x; e < p.d; e += blockDim.x) {
+    Acc a = 0;
+    for (int s = 0; s < ns; ++s) a += static_cast<Acc>(w_s[s]) * acc[(int64_t)s * p.d + e];
+    out[e] = E::from_acc(a / static_cast<Acc>(L));
+  }
+}
+
+template <typename T>
+int launch_generic(const DecodeParams &p, hipStream_t stream) {
+  using Acc = typename Elem<T>::acc;
+  const int nhc = static_cast<int>(ceil_div(p.group, kGenHeads));
+  dim3 grid(p.max_splits, p.hkv * nhc, p.batch);
+  const size_t lds = sizeof(Acc) * kGenHeads * p.d + sizeof(int64_t) * p.ts +
+                     sizeof(float) * kGenHeads * p.ts;
+  decode_split_generic<T><<<grid, 256, lds, stream>>>(p);
+  int rc = check_launch("mlr_paged_decode(split)");
+  if (rc != MLR_OK) return rc;
+  return launch_combine<T>(p, stream);
+}
+
+}  // namespace
+
+template <typename T>
+int launch_combine(const DecodeParams &p, hipStream_t stream) {
+  dim3 grid(p.hq, p.batch);
+  const size_t lds = sizeof(float) * p.max_splits;
+  decode_combine<T><<<grid, 256, lds, stream>>>(p);
+  return check_launch("mlr_paged_decode(combine)");
+}
+
+template int launch_combine<bf16_t>(const DecodeParams &, hipStream_t);
+
+int64_t default_tokens_per_split(int dtype, int64_t head_dim) {
+  // The bf16 MFMA kernel streams tiles, so longer splits only cost parallelism;
+  // the generic kernel holds a split's scores in LDS (<= kGenMaxSplit).
+  if (dtype == MLR_DTYPE_BF16 && (head_dim == 64 || head_dim == 128)) return 512;
+  return 256;
+}
+
+DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
+                                        int64_t max_splits, int dtype) {
+  DecodeWorkspace w;
+  const int64_t rows = batch * hq * max_splits;
+  w.ml_bytes = rows * static_cast<int64_t>(sizeof(float2));
+  w.acc_offset = (w.ml_bytes + 255) / 256 * 256;
+  const int64_t acc_elem = dtype == MLR_DTYPE_F64 ? 8 : 4;
+  w.total = w.acc_offset + rows * d * acc_elem;
+  return w;
+}
+
+}  // namespace mlr
+
+using namespace mlr;
+
+extern "C" size_t mlr_paged_decode_workspace_size(int64_t batch,
+                                                  int64_t num_q_heads,
+                                                  int64_t head_dim,
+                                                  int64_t max_context,
+                                                  int64_t tokens_per_split,
+                                                  int dtype) {
+  if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_context <= 0)
+    return 0;
+  const int64_t ts = tokens_per_split > 0
+                         ? tokens_per_split
+                         : default_tokens_per_split(dtype, head_dim);
+  const int64_t splits = ceil_div(max_context, ts);
+  return static_cast<size_t>(
+      decode_workspace_layout(batch, num_q_heads, head_dim, splits, dtype).total);
+}
+
+extern "C" int mlr_paged_decode(
+    const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *k_cache,
+    const void *v_cache, int64_t num_blocks, int64_t block_size,
+    int64_t num_kv_heads, int64_t head_dim, const int64_t *block_tables,
+    int64_t block_table_stride, int64_t max_blocks_per_seq,
+    const int64_t *context_lens, int64_t batch, int64_t num_q_heads,
+    double scale, int dtype, int64_t tokens_per_split, void *workspace,
+    size_t workspace_bytes, void *out, int64_t out_stride_b,
+    int64_t out_stride_h, void *stream) {
+  clear_error();
+  MLR_REQUIRE(batch > 0, "mlr_paged_decode: batch must be > 0");
+  MLR_REQUIRE(num_kv_heads > 0 && num_q_heads > 0,
+              "mlr_paged_decode: head counts must be > 0");
+  MLR_REQUIRE(num_q_heads % num_kv_heads == 0,
+              "mlr_paged_decode: num_q_heads must be divisible by num_kv_heads");
+  MLR_REQUIRE(head_dim > 0 && head_dim <= 1024,
+              "mlr_paged_decode: head_dim must be in [1, 1024]");
+  MLR_REQUIRE(block_size > 0 && num_blocks > 0,
+              "mlr_paged_decode: block_size and num_blocks must be > 0");
+  MLR_REQUIRE(max_blocks_per_seq > 0,
+              "mlr_paged_decode: block tables must have at least one column");
+  MLR_REQUIRE(block_table_stride >= max_blocks_per_seq,
+              "mlr_paged_decode: block_table_stride < max_blocks_per_seq");
+  MLR_REQUIRE(q && k_cache && v_cache && block_tables && context_lens && out,
+              "mlr_paged_decode: null pointer argument");
+  MLR_REQUIRE(dtype_size(dtype) > 0, "mlr_paged_decode: unknown dtype %d", dtype);
+  MLR_REQUIRE(batch <= 65535 && num_kv_heads * num_q_heads <= (1 << 20),
+              "mlr_paged_decode: batch or head count too large for the grid");
+
+  const int64_t max_context = max_blocks_per_seq * block_size;
+  // The MFMA kernel moves 16-byte Q and K fragments and 8/16-byte V fragments.
+  const bool aligned = (reinterpret_cast<uintptr_t>(q) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 &&
+                       q_stride_b % 8 == 0 && q_stride_h % 8 == 0;
+  const bool mfma =
+      aligned && decode_mfma_eligible(dtype, head_dim,
+                                      num_q_heads / num_kv_heads, block_size);
+  int64_t ts = tokens_per_split > 0 ? tokens_per_split
+                                    : default_tokens_per_split(dtype, head_dim);
+  if (!mfma) {
+    MLR_REQUIRE(ts <= kGenMaxSplit,
+                "mlr_paged_decode: tokens_per_split %lld exceeds %d for this "
+                "dtype/shape", (long long)ts, kGenMaxSplit);
+    MLR_REQUIRE(head_dim <= 512,
+                "mlr_paged_decode: head_dim > 512 is not supported");
+  } else {
+    MLR_REQUIRE(ts % 16 == 0,
+                "mlr_paged_decode: tokens_per_split must be a multiple of 16");
+  }
+  const int64_t max_splits = ceil_div(max_context, ts);
+  MLR_REQUIRE(max_splits <= 8192,
+              "mlr_paged_decode: %lld splits exceed the combine limit of 8192; "
+              "raise tokens_per_split", (long long)max_splits);
+  const DecodeWorkspace wl =
+      decode_workspace_layout(batch, num_q_heads, head_dim, max_splits, dtype);
+  if (!workspace || workspace_bytes < static_cast<size_t>(wl.total)) {
+    return set_error(MLR_ERR_WORKSPACE,
+                     "mlr_paged_decode: workspace of %zu bytes is smaller than "
+                     "the %lld bytes required",
+                     workspace_bytes, (long long)wl.total);
+  }
+  MLR_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
+              "mlr_paged_decode: workspace must be 256-byte aligned");
+
+  DecodeParams p{};
+  p.q = q;
+  p.q_sb = q_stride_b;
+  p.q_sh = q_stride_h;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.num_blocks = num_blocks;
+  p.block_size = block_size;
+  p.hkv = static_cast<int>(num_kv_heads);
+  p.d = static_cast<int>(head_dim);
+  p.bt = block_tables;
+  p.bt_stride = block_table_stride;
+  p.max_blocks = max_blocks_per_seq;
+  p.ctx = context_lens;
+  p.batch = static_cast<int>(batch);
+  p.hq = static_cast<int>(num_q_heads);
+  p.group = static_cast<int>(num_q_heads / num_kv_heads);
+  p.scale = scale;
+  p.ts = static_cast<int>(ts);
+  p.max_splits = static_cast<int>(max_splits);
+  p.ws_ml = static_cast<float2 *>(workspace);
+  p.ws_acc = static_cast<unsigned char *>(workspace) + wl.acc_offset;
+  p.out = out;
+  p.o_sb = out_stride_b;
+  p.o_sh = out_stride_h;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mfma) return launch_decode_mfma(p, s);
+  switch (dtype) {
+    case MLR_DTYPE_F32: return launch_generic<float>(p, s);
+    case MLR_DTYPE_F16: return launch_generic<f16_t>(p, s);
+    case MLR_DTYPE_BF16: return launch_generic<bf16_t>(p, s);
+    case MLR_DTYPE_F64: return launch_generic<double>(p, s);
+    default: return set_error(MLR_ERR_INVALID, "mlr_paged_decode: bad dtype");
+  }
+}

@@ -1,0 +1,178 @@
+"""Checks that pin the oracle's attention restatements to independent answers.
+
+Each ``check_*`` takes an oracle module (``oracle.paged_attention`` or a
+mutant of it) and raises AssertionError when the module disagrees with:
+- the reference's stored masked-SDPA known answer (tests/golden), or
+- the float64 textbook attention of ``oracle.textbook`` on paged layouts.
+tests/test_oracle_pins.py runs them on the oracle; tests/test_oracle_mutants.py
+plants mistakes in copies of the oracle and requires every mistake to fail.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import torch
+
+from oracle import textbook
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load_kat():
+    with np.load(os.path.join(GOLDEN, "sdpa_known_answer.npz"), allow_pickle=False) as z:
+        return {name: np.array(z[name]) for name in z.files}
+
+
+def build_pool(logical_k, logical_v, block_table, block_size, num_blocks, fill=float("nan")):
+    """Scatter logical [S, Hkv, D] rows into a NaN-filled [NB, BS, Hkv, D] pool."""
+    shape = (num_blocks, block_size) + tuple(logical_k.shape[1:])
+    k_cache = torch.full(shape, fill, dtype=logical_k.dtype)
+    v_cache = torch.full(shape, fill, dtype=logical_v.dtype)
+    for pos in range(logical_k.shape[0]):
+        blk = block_table[pos // block_size]
+        k_cache[blk, pos % block_size] = logical_k[pos]
+        v_cache[blk, pos % block_size] = logical_v[pos]
+    return k_cache, v_cache
+
+
+def kat_rows():
+    """(q [1,64], visible K [n,1,64], visible V [n,1,64], expected [64]) per KAT row."""
+    kat = load_kat()
+    rows = []
+    for b in range(kat["q"].shape[0]):
+        for i in range(kat["q"].shape[1]):
+            cols = np.nonzero(kat["mask"][b, i])[0]
+            rows.append((torch.from_numpy(kat["q"][b, i][None, :]),
+                         torch.from_numpy(kat["k"][b, cols][:, None, :]),
+                         torch.from_numpy(kat["v"][b, cols][:, None, :]),
+                         kat["expected"][b, i]))
+    return rows
+
+
+def _table(n_blocks, num_blocks, gen):
+    return torch.randperm(num_blocks, generator=gen)[:n_blocks].tolist()
+
+
+def check_decode_vs_kat(mod):
+    gen = torch.Generator().manual_seed(7)
+    block_size, num_blocks = 4, 8
+    qs, tables, lens, pools_k, pools_v, expected = [], [], [], [], [], []
+    for q, k, v, exp in kat_rows():
+        table = _table((k.shape[0] + block_size - 1) // block_size, num_blocks, gen)
+        kc, vc = build_pool(k, v, table, block_size, num_blocks)
+        out = mod.decode_single(q, kc, vc, table, k.shape[0], block_size)
+        np.testing.assert_allclose(out[0].numpy(), exp, rtol=1e-4, atol=1e-5)
+        # The tensorized path gathers block 0 for padded positions and
+        # multiplies them by zero probability (reference :230-253), so its
+        # pools hold finite filler instead of NaN.
+        kc, vc = build_pool(k, v, table, block_size, num_blocks, fill=1e3)
+        qs.append(q)
+        tables.append(table)
+        lens.append(k.shape[0])
+        pools_k.append(kc)
+        pools_v.append(vc)
+        expected.append(exp)
+    # The same rows as one ragged batch over one shared pool.
+    offsets, shared_k, shared_v, shifted = 0, [], [], []
+    for table, kc, vc in zip(tables, pools_k, pools_v):
+        shared_k.append(kc)
+        shared_v.append(vc)
+        shifted.append([b + offsets for b in table])
+        offsets += num_blocks
+    width = max(len(t) for t in shifted)
+    bt = torch.tensor([t + [-1] * (width - len(t)) for t in shifted])
+    out = mod.decode_batch_parallel(torch.stack([q for q in qs]), torch.cat(shared_k),
+                                    torch.cat(shared_v), bt, torch.tensor(lens), block_size)
+    np.testing.assert_allclose(out[:, 0].numpy(), np.stack(expected), rtol=1e-4, atol=1e-5)
+
+
+def check_prefill_vs_kat(mod):
+    """A one-token chunk whose context is the row's visible keys is that row."""
+    gen = torch.Generator().manual_seed(11)
+    block_size, num_blocks = 4, 8
+    for q, k, v, exp in kat_rows()[::3]:
+        n = k.shape[0]
+        table = _table((n + block_size - 1) // block_size, num_blocks, gen)
+        kc, vc = build_pool(k, v, table, block_size, num_blocks)
+        for fn, tile in ((mod.prefill_chunk_tiled, 3), (mod.prefill_chunk_dense, 1)):
+            out = fn(q[None], kc, vc, table, n - 1, n, block_size, tile)
+            np.testing.assert_allclose(out[0, 0].numpy(), exp, rtol=1e-4, atol=1e-5)
+
+
+def random_paged(seq_lens, hq, hkv, d, block_size, dtype=torch.float32, seed=0,
+                 spare_blocks=3, fill=float("nan")):
+    """Random q and filler-padded pools with shuffled, -1-padded block tables."""
+    gen = torch.Generator().manual_seed(seed)
+    need = [(s + block_size - 1) // block_size for s in seq_lens]
+    num_blocks = sum(need) + spare_blocks
+    perm = torch.randperm(num_blocks, generator=gen).tolist()
+    k_cache = torch.full((num_blocks, block_size, hkv, d), fill, dtype=dtype)
+    v_cache = torch.full_like(k_cache, fill)
+    tables, cursor = [], 0
+    for s, n in zip(seq_lens, need):
+        table = perm[cursor:cursor + n]
+        cursor += n
+        tables.append(table)
+        k = torch.randn(s, hkv, d, generator=gen).to(dtype)
+        v = torch.randn(s, hkv, d, generator=gen).to(dtype)
+        for pos in range(s):
+            k_cache[table[pos // block_size], pos % block_size] = k[pos]
+            v_cache[table[pos // block_size], pos % block_size] = v[pos]
+    width = max(need)
+    bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.long)
+    q = torch.randn(len(seq_lens), hq, d, generator=gen).to(dtype)
+    return q, k_cache, v_cache, bt, torch.tensor(seq_lens, dtype=torch.long), tables
+
+
+def check_decode_vs_textbook(mod):
+    for hq, hkv, lens, d, bs in (
+        (14, 2, [17, 64, 130, 255], 64, 16),   # FP32 decode workload, GQA 7:1
+        (4, 4, [3, 9], 8, 4),                  # MHA
+        (4, 1, [5, 1], 8, 2),                  # MQA, one-token context
+        (6, 2, [33], 16, 8),
+    ):
+        q, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, bs, seed=hq * 100 + d,
+                                                 fill=1e3)
+        want = textbook.paged_decode(q.numpy(), kc.numpy(), vc.numpy(), tables, lens)
+        got = mod.decode_batch_parallel(q, kc, vc, bt, sl, bs)
+        np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-5)
+        for b in range(len(lens)):
+            single = mod.decode_single(q[b], kc, vc, tables[b], lens[b], bs)
+            np.testing.assert_allclose(single.numpy(), want[b], rtol=1e-5, atol=1e-5)
+
+
+def check_prefill_vs_textbook(mod):
+    # The reference test grid (tests/kernels/test_paged_attention.py:249-351),
+    # plus a multi-block GQA 7:1 case.
+    cases = []
+    for hq, hkv in ((2, 2), (4, 2), (4, 1)):
+        for prefix in (0, 5):
+            for tile in (1, 4, 16):
+                cases.append((hq, hkv, prefix, 4, 8, 3, tile))
+    cases.append((14, 2, 37, 21, 64, 16, 16))
+    for hq, hkv, prefix, chunk, d, bs, tile in cases:
+        gen = torch.Generator().manual_seed(prefix * 31 + tile + hq)
+        context = prefix + chunk
+        n_blocks = (context + bs - 1) // bs
+        table = torch.randperm(n_blocks + 2, generator=gen)[:n_blocks].tolist()
+        k = torch.randn(context, hkv, d, generator=gen)
+        v = torch.randn(context, hkv, d, generator=gen)
+        q = torch.randn(chunk, hq, d, generator=gen)
+        kc, vc = build_pool(k, v, table, bs, n_blocks + 2)
+        want = textbook.paged_prefill(q.numpy(), kc.numpy(), vc.numpy(), table, prefix)
+        for fn in (mod.prefill_chunk_tiled, mod.prefill_chunk_dense):
+            got = fn(q, kc, vc, table, prefix, context, bs, tile)
+            np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-5)
+        # BF16 inputs: within the reference test's BF16 tolerance of the
+        # textbook answer on the same (rounded) values.
+        qb, kcb, vcb = q.bfloat16(), kc.bfloat16(), vc.bfloat16()
+        want_b = textbook.paged_prefill(qb.float().numpy(), kcb.float().numpy(),
+                                        vcb.float().numpy(), table, prefix)
+        got_b = mod.prefill_chunk_tiled(qb, kcb, vcb, table, prefix, context, bs, tile)
+        np.testing.assert_allclose(got_b.float().numpy(), want_b, rtol=1e-2, atol=2e-2)
+
+
+ALL_CHECKS = (check_decode_vs_kat, check_prefill_vs_kat, check_decode_vs_textbook,
+              check_prefill_vs_textbook)

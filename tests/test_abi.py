@@ -1,0 +1,81 @@
+"""The C-ABI library loads and exports every function include/mlr_attn.h declares.
+
+Runs without a GPU: loading the library and calling its argument checks never
+reaches the HIP runtime (every call below fails validation before a launch).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from mini_llm_runtime_amd import _lib
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "mlr_attn.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mlr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for name in ("mlr_kv_write", "mlr_paged_decode", "mlr_paged_prefill",
+                 "mlr_paged_prefill_chunk", "mlr_paged_decode_workspace_size",
+                 "mlr_last_error", "mlr_version"):
+        assert name in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in mlr_attn.h but not exported"
+    # The Python prototypes cover the header exactly.
+    assert sorted(_lib.EXPORTED_SYMBOLS) == declared_functions()
+
+
+def test_loader_binds_prototypes():
+    lib = _lib.load()
+    assert lib.mlr_version() >= 100
+    assert lib.mlr_last_error() == b""
+
+
+def test_workspace_size_is_host_arithmetic():
+    lib = _lib.load()
+    # bf16, D=64: 512-token splits; 64 x 14 heads x 8 splits of (m, l) + acc.
+    size = lib.mlr_paged_decode_workspace_size(64, 14, 64, 4096, 0, 2)
+    rows = 64 * 14 * 8
+    ml = rows * 8
+    assert size == (ml + 255) // 256 * 256 + rows * 64 * 4
+    assert lib.mlr_paged_decode_workspace_size(0, 14, 64, 4096, 0, 2) == 0
+
+
+@pytest.mark.parametrize("call,needle", [
+    (lambda lib: lib.mlr_kv_write(None, None, 0, -1, 0, 0, 0, 0, 0, 0, None, 1,
+                                  None, None, 0, 16, 2, 64, None), b"num_tokens"),
+    (lambda lib: lib.mlr_kv_write(None, None, 9, 1, 0, 0, 0, 0, 0, 0, None, 1,
+                                  None, None, 0, 16, 2, 64, None), b"source dtype"),
+    (lambda lib: lib.mlr_paged_decode(None, 0, 0, None, None, 8, 16, 3, 64, None, 4, 4,
+                                      None, 2, 14, 0.125, 2, 0, None, 0, None, 0, 0,
+                                      None), b"divisible"),
+    (lambda lib: lib.mlr_paged_prefill(None, 0, 0, None, None, 8, 16, 2, 300, None, 4, 4,
+                                       None, None, 1, 4, 14, 0.125, 2, 64, None, 0, 0,
+                                       None), b"head_dim"),
+])
+def test_argument_errors_return_before_any_launch(call, needle):
+    lib = _lib.load()
+    assert call(lib) == 1  # MLR_ERR_INVALID
+    assert needle in lib.mlr_last_error()
+
+
+def test_empty_kv_write_is_a_no_op():
+    lib = _lib.load()
+    assert lib.mlr_kv_write(None, None, 2, 0, 0, 0, 0, 0, 0, 0, None, 1, None, None,
+                            2, 16, 2, 64, None) == 0

@@ -1,0 +1,123 @@
+"""Paged chunk prefill on the GPU against the oracle's tiled restatement (CPU).
+
+Tolerances (max-abs): 1e-5 for FP32/FP64, 2e-2 for BF16/FP16 (FP32 softmax).
+Pools are NaN-filled outside the written context, so a stray read fails.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle.paged_attention as opa
+from mini_llm_runtime_amd import workloads
+from mini_llm_runtime_amd.kernels import paged_attention as kpa
+from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+from oracle_pins import build_pool
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.float64: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def max_abs(a, b):
+    return (a.double().cpu() - b.double().cpu()).abs().max().item()
+
+
+def make_case(hq, hkv, prefix, chunk, d, bs, dtype, seed, spare=2):
+    gen = torch.Generator().manual_seed(seed)
+    context = prefix + chunk
+    n_blocks = (context + bs - 1) // bs
+    table = torch.randperm(n_blocks + spare, generator=gen)[:n_blocks].tolist()
+    k = torch.randn(context, hkv, d, generator=gen).to(dtype)
+    v = torch.randn(context, hkv, d, generator=gen).to(dtype)
+    q = torch.randn(chunk, hq, d, generator=gen).to(dtype)
+    kc, vc = build_pool(k, v, table, bs, n_blocks + spare)
+    return q, kc, vc, table
+
+
+@pytest.mark.parametrize("hq,hkv", [(2, 2), (4, 2), (4, 1)], ids=["mha", "gqa", "mqa"])
+@pytest.mark.parametrize("prefix", [0, 5], ids=["first-chunk", "with-prefix"])
+@pytest.mark.parametrize("tile", [1, 4, 16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_reference_chunk_grid(device, hq, hkv, prefix, tile, dtype):
+    # The reference's grid (tests/kernels/test_paged_attention.py:249-351).
+    q, kc, vc, table = make_case(hq, hkv, prefix, 4, 8, 3, dtype, seed=0)
+    want = opa.prefill_chunk_tiled(q, kc, vc, table, prefix, prefix + 4, 3, tile)
+    got = kpa.paged_attention_prefill_chunk_tiled(
+        q.to(device), kc.to(device), vc.to(device), table, prefix, prefix + 4, 3, tile)
+    assert got.shape == q.shape and got.dtype == q.dtype
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) <= TOL[dtype]
+
+
+CASES = [
+    # (dtype, hq, hkv, d, bs, prefix, chunk, tile)
+    (torch.bfloat16, 14, 2, 64, 16, 0, 512, 64),
+    (torch.bfloat16, 14, 2, 64, 16, 1000, 77, 128),
+    (torch.bfloat16, 28, 4, 128, 16, 300, 200, 16),
+    (torch.bfloat16, 8, 8, 64, 32, 17, 100, 64),
+    (torch.float16, 14, 2, 64, 16, 100, 130, 64),
+    (torch.float32, 14, 2, 64, 16, 250, 70, 64),
+    (torch.float32, 6, 3, 40, 5, 11, 29, 7),
+    (torch.float64, 4, 2, 16, 4, 9, 13, 4),
+]
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d,bs,prefix,chunk,tile", CASES,
+                         ids=[f"{str(c[0])[6:]}-{c[1]}x{c[2]}-d{c[3]}-p{c[5]}-c{c[6]}"
+                              for c in CASES])
+def test_chunk_matches_oracle(device, dtype, hq, hkv, d, bs, prefix, chunk, tile):
+    q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, dtype, seed=chunk)
+    want = opa.prefill_chunk_tiled(q, kc, vc, table, prefix, prefix + chunk, bs, tile)
+    got = kpa.paged_attention_prefill_chunk_tiled(
+        q.to(device), kc.to(device), vc.to(device), table, prefix, prefix + chunk, bs, tile)
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("tile", [16, 64, 128])
+def test_chunk512_x8_varlen_with_kv_write(device, tile):
+    """BF16 chunk prefill, 8 sequences x 512-token chunk, prefixes U[0, 3584]."""
+    wl = workloads.bf16_prefill_chunk512_x8()
+    nb = wl.k_cache.shape[0]
+    cache = PagedKVCache(1, nb, 16, 2, 64, dtype=torch.bfloat16, device=device)
+    cache.k_cache[0].copy_(wl.k_cache)
+    cache.v_cache[0].copy_(wl.v_cache)
+    cache.write_slots(wl.slot_mapping.to(device), wl.chunk_k.to(device),
+                      wl.chunk_v.to(device))
+    kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
+    kc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_k)
+    vc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_v)
+    assert torch.equal(cache.k_cache[0].cpu(), kc)
+    k_layer, v_layer = cache.get_layer_cache(0)
+    got = kpa.paged_attention_prefill_varlen(
+        wl.q.to(device), k_layer, v_layer, wl.block_tables.to(device),
+        wl.query_start_loc.to(device), wl.context_lens.to(device), 16, tile).cpu()
+    worst = 0.0
+    for s in (0, 3, 7):
+        lo, hi = int(wl.query_start_loc[s]), int(wl.query_start_loc[s + 1])
+        p = wl.prefix_lens[s]
+        want = opa.prefill_chunk_tiled(wl.q[lo:hi], kc, vc, wl.tables[s], p, p + hi - lo,
+                                       16, tile)
+        worst = max(worst, max_abs(got[lo:hi], want))
+    print(f"chunk512_x8 tile {tile}: max-abs vs oracle {worst:.3e}")
+    assert worst <= 2e-2
+
+
+def test_varlen_equals_per_sequence_calls(device):
+    """Packing sequences into one launch changes nothing, bit for bit."""
+    wl = workloads.bf16_prefill_chunk512_x8(num_seqs=3, chunk=96, max_prefix=300)
+    kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
+    kc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_k)
+    vc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_v)
+    kc, vc = kc.to(device), vc.to(device)
+    packed = kpa.paged_attention_prefill_varlen(
+        wl.q.to(device), kc, vc, wl.block_tables.to(device), wl.query_start_loc.to(device),
+        wl.context_lens.to(device), 16, 64)
+    for s in range(3):
+        lo, hi = int(wl.query_start_loc[s]), int(wl.query_start_loc[s + 1])
+        p = wl.prefix_lens[s]
+        single = kpa.paged_attention_prefill_chunk_tiled(
+            wl.q[lo:hi].to(device), kc, vc, wl.tables[s], p, p + hi - lo, 16, 64)
+        assert torch.equal(single, packed[lo:hi])

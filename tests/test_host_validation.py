@@ -1,0 +1,144 @@
+"""Host-side checks of the drop-in API (CPU; no kernel is launched).
+
+The product functions raise the reference's errors for bad arguments, check
+everything before touching the cache, and refuse CPU tensors instead of
+falling back to PyTorch math.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mini_llm_runtime_amd.kernels import paged_attention as kpa
+from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+
+
+def test_write_slots_valid_call_on_cpu_refuses_to_fall_back():
+    cache = PagedKVCache(2, 3, 4, 2, 8, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="only on HIP devices"):
+        cache.write_slots(torch.tensor([1, 2]), torch.randn(2, 2, 8), torch.randn(2, 2, 8),
+                          layer_idx=1)
+
+
+@pytest.mark.parametrize("slots,error,message", [
+    ([0, 0], ValueError, "distinct"),
+    ([0, -1], IndexError, "out-of-range"),
+    ([0, 12], IndexError, "out-of-range"),
+    ([0.0, 1.0], TypeError, "integer"),
+])
+def test_invalid_slot_write_does_not_modify_cache(slots, error, message):
+    # tests/runtime/test_write_slots_batch.py:39-55 of the reference.
+    cache = PagedKVCache(2, 3, 4, 2, 8, dtype=torch.float32)
+    cache.k_cache.fill_(17)
+    cache.v_cache.fill_(23)
+    with pytest.raises(error, match=message):
+        cache.write_slots(torch.tensor(slots), torch.randn(2, 2, 8), torch.randn(2, 2, 8),
+                          layer_idx=1)
+    assert torch.all(cache.k_cache == 17) and torch.all(cache.v_cache == 23)
+
+
+@pytest.mark.parametrize("layer_idx", [-1, 2])
+def test_write_slots_rejects_layer(layer_idx):
+    cache = PagedKVCache(2, 2, 4, 2, 8, dtype=torch.float32)
+    with pytest.raises(IndexError, match="layer_idx"):
+        cache.write_slots(torch.tensor([1]), torch.randn(1, 2, 8), torch.randn(1, 2, 8),
+                          layer_idx=layer_idx)
+
+
+def test_write_slots_rejects_non_3d():
+    cache = PagedKVCache(2, 2, 4, 2, 8, dtype=torch.float32)
+    with pytest.raises(ValueError, match="Expected K/V shape"):
+        cache.write_slots(torch.tensor([0, 1]), torch.randn(2, 8), torch.randn(2, 8), 0)
+
+
+def test_empty_write_is_allowed_on_any_device():
+    cache = PagedKVCache(1, 2, 4, 2, 8, dtype=torch.float32)
+    cache.write_slots(torch.tensor([], dtype=torch.long), torch.randn(0, 2, 8),
+                      torch.randn(0, 2, 8))
+
+
+def test_allocator_matches_reference_behaviour():
+    cache = PagedKVCache(1, 3, 2, 1, 4)
+    cache.add_sequence("A")
+    assert cache.reserve_tokens("A", 3) is True and cache.block_tables["A"] == [0, 1]
+    assert cache.reserve_tokens("A", 4) is True and len(cache.free_blocks) == 1
+    cache.add_sequence("B")
+    assert cache.reserve_tokens("B", 3) is False and cache.block_tables["B"] == []
+    cache.free_sequence("A")
+    assert cache.reserve_tokens("B", 3) is True and cache.block_tables["B"] == [1, 0]
+    with pytest.raises(KeyError):
+        cache.add_sequence("B")
+    with pytest.raises(ValueError, match="negative"):
+        cache.reserve_tokens("B", -1)
+
+
+def test_cpu_append_helpers_keep_reference_semantics():
+    cache = PagedKVCache(1, 8, 4, 2, 8, dtype=torch.float32)
+    cache.add_sequence(0)
+    prompt_k, prompt_v = torch.randn(8, 2, 8), torch.randn(8, 2, 8)
+    cache.append_tokens(0, prompt_k, prompt_v)
+    cache.append(0, torch.randn(2, 8), torch.randn(2, 8))
+    assert cache.seq_lens[0] == 9 and len(cache.block_tables[0]) == 3
+    got_k, _ = cache.get_sequence(0)
+    torch.testing.assert_close(got_k[:8], prompt_k)
+    small = PagedKVCache(1, 2, 4, 2, 8, dtype=torch.float32)
+    small.add_sequence(0)
+    with pytest.raises(RuntimeError):
+        small.append_tokens(0, torch.randn(10, 2, 8), torch.randn(10, 2, 8))
+    assert small.block_tables[0] == [] and len(small.free_blocks) == 2
+
+
+def _decode_args():
+    q = torch.randn(2, 4, 8)
+    k = torch.randn(5, 2, 2, 8)
+    return q, k, torch.randn_like(k), torch.tensor([[2, 0, -1], [1, 3, 4]]), torch.tensor([3, 5])
+
+
+@pytest.mark.parametrize("mutate,error,message", [
+    (lambda a: (a[0][0],) + a[1:], ValueError, r"q must have shape \[B, Hq, D\]"),
+    (lambda a: (a[0], a[1][0]) + a[2:], ValueError, "k_cache and v_cache must have shape"),
+    (lambda a: (a[0], a[1], a[2][:4]) + a[3:], ValueError, "same shape"),
+    (lambda a: (a[0][..., :4],) + a[1:], ValueError, "same head_dim"),
+    (lambda a: (torch.randn(2, 3, 8),) + a[1:], ValueError, "divisible"),
+    (lambda a: a[:3] + (a[3][:1],) + a[4:], ValueError, "block_tables length"),
+    (lambda a: a[:4] + (a[4][:1],), ValueError, "seq_lens length"),
+])
+def test_batch_decode_validation_messages(mutate, error, message):
+    args = mutate(_decode_args())
+    with pytest.raises(error, match=message):
+        kpa.paged_attention_decode_batch_parallel(*args, block_size=2)
+
+
+def test_batch_decode_on_cpu_refuses_to_fall_back():
+    with pytest.raises(RuntimeError, match="only on HIP devices"):
+        kpa.paged_attention_decode_batch_parallel(*_decode_args(), block_size=2)
+
+
+def test_single_decode_validation_messages():
+    q, k, v = torch.randn(4, 8), torch.randn(2, 4, 2, 8), torch.randn(2, 4, 2, 8)
+    with pytest.raises(ValueError, match="greater than 0"):
+        kpa.paged_attention_decode(q, k, v, [0], 0, 4)
+    with pytest.raises(ValueError, match="enough blocks"):
+        kpa.paged_attention_decode(q, k, v, [0], 5, 4)
+    with pytest.raises(ValueError, match="block_size does not match"):
+        kpa.paged_attention_decode(q, k, v, [0, 1, 0], 5, 2)
+    with pytest.raises(ValueError, match="divisible"):
+        kpa.paged_attention_decode(torch.randn(3, 8), k, v, [0], 3, 4)
+    with pytest.raises(RuntimeError, match="only on HIP devices"):
+        kpa.paged_attention_decode(q, k, v, [1, 0], 5, 4)
+
+
+def test_chunk_prefill_validation_messages():
+    q = torch.randn(4, 4, 8)
+    k = torch.randn(4, 3, 2, 8)
+    v = torch.randn_like(k)
+    with pytest.raises(ValueError, match="tile_size must be greater than 0"):
+        kpa.paged_attention_prefill_chunk_tiled(q, k, v, [2, 0, 3], 5, 9, 3, 0)
+    with pytest.raises(ValueError, match="context_len must equal"):
+        kpa.paged_attention_prefill_chunk_tiled(q, k, v, [2, 0, 3], 5, 8, 3, 4)
+    with pytest.raises(ValueError, match="divisible"):
+        kpa.paged_attention_prefill_chunk_tiled(torch.randn(4, 3, 8), k, v, [2, 0, 3], 5,
+                                                9, 3, 4)
+    with pytest.raises(RuntimeError, match="only on HIP devices"):
+        kpa.paged_attention_prefill_chunk_tiled(q, k, v, [2, 0, 3], 5, 9, 3, 4)

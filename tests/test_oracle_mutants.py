@@ -1,0 +1,78 @@
+"""Plant plausible mistakes in copies of the oracle; the pins must catch each.
+
+A mutant is oracle/paged_attention.py with one source edit, executed as a
+fresh module on the CPU. If no pin check fails for a mutant, the pins would
+not notice that mistake in the oracle either, and this test fails.
+"""
+
+from __future__ import annotations
+
+import inspect
+import types
+
+import pytest
+
+import oracle.paged_attention as pa
+
+import oracle_pins
+
+MUTATIONS = {
+    # GQA: query head h reads KV head h % Hkv instead of h // group.
+    "gqa-map-tiled-not-interleaved": (
+        "k = k_cache[physical, offsets].transpose(1, 2).repeat_interleave(group, dim=1)\n"
+        "    v = v_cache[physical, offsets].transpose(1, 2).repeat_interleave(group, dim=1)",
+        "k = k_cache[physical, offsets].transpose(1, 2).repeat(1, group, 1, 1)\n"
+        "    v = v_cache[physical, offsets].transpose(1, 2).repeat(1, group, 1, 1)",
+    ),
+    "dropped-decode-scale": (
+        "scores = torch.matmul(q.unsqueeze(2), k.transpose(-2, -1)) * scale",
+        "scores = torch.matmul(q.unsqueeze(2), k.transpose(-2, -1))",
+    ),
+    "length-mask-off-by-one": (
+        "live = pos.unsqueeze(0) < seq_lens.unsqueeze(1)",
+        "live = pos.unsqueeze(0) < seq_lens.unsqueeze(1) - 1",
+    ),
+    "block-offset-swapped": (
+        "keys.append(k_cache[block][pos % block_size])",
+        "keys.append(k_cache[block][(pos + 1) % block_size])",
+    ),
+    "causal-mask-strict": (
+        "visible = positions.unsqueeze(0) <= query_pos.unsqueeze(1)\n"
+        "        scores = scores.to(torch.float32)",
+        "visible = positions.unsqueeze(0) < query_pos.unsqueeze(1)\n"
+        "        scores = scores.to(torch.float32)",
+    ),
+    "online-rescale-dropped": (
+        "acc = acc * rescale + weights @ values.to(torch.float32)",
+        "acc = acc + weights @ values.to(torch.float32)",
+    ),
+    "prefill-prefix-ignored": (
+        "query_pos = prefix_len + torch.arange(chunk, device=q.device)",
+        "query_pos = torch.arange(chunk, device=q.device)",
+    ),
+    "dense-slot-uses-offset-only": (
+        "return table[positions // block_size] * block_size + positions % block_size",
+        "return table[positions // block_size] * block_size",
+    ),
+}
+
+
+def make_mutant(name: str) -> types.ModuleType:
+    before, after = MUTATIONS[name]
+    source = inspect.getsource(pa)
+    assert source.count(before) == 1, f"mutation site for {name} not found exactly once"
+    module = types.ModuleType(f"oracle_mutant_{name}")
+    exec(compile(source.replace(before, after), module.__name__, "exec"), module.__dict__)
+    return module
+
+
+@pytest.mark.parametrize("name", sorted(MUTATIONS))
+def test_pins_catch_planted_mistake(name):
+    mutant = make_mutant(name)
+    caught = []
+    for check in oracle_pins.ALL_CHECKS:
+        try:
+            check(mutant)
+        except (AssertionError, IndexError, RuntimeError, ValueError):
+            caught.append(check.__name__)
+    assert caught, f"no pin detects the planted mistake {name!r}"
