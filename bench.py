@@ -1,0 +1,341 @@
+"""Benchmark of the paged attention hot path on one MI355X.
+
+One step = the decode step of one attention layer at Qwen2.5-0.5B shape
+(bf16_decode_qwen05b_b64: batch 64, 14 q / 2 KV heads, head_dim 64, block 16,
+contexts U[128, 4096], 24576-block pool): the batched KV write of the 64 new
+tokens through slot_mapping, then split-KV paged decode (split + combine).
+
+Timing: inputs are resident in HBM. Consecutive steps use consecutive layers
+of a 24-layer cache (24 distinct 201 MB K+V pools, 4.8 GB), so a layer's pool
+is evicted from the 256 MB Infinity Cache (MALL) before it is read again and
+the figure is an HBM figure. The steps are captured once into a HIP graph of
+24 steps and replayed; HIP events on the launch stream bracket exactly
+``--steps`` steps. ``value`` is whole-step algorithmic bytes / time.
+
+The roofline object is for the dominant kernel call, mlr_paged_decode (split
++ combine kernels): its algorithmic bytes (K and V rows of every context
+token, q, out, block ids, lengths) over its own event-timed average duration,
+against the 8 TB/s HBM peak.
+
+The CPU baseline times the oracle (a CPU restatement of the reference's
+PyTorch path: write_slots + paged_attention_decode_batch_parallel) on the
+same inputs with all host cores.
+
+A secondary object reports BF16 chunk prefill (8 x 512-token chunks on
+prefixes U[0, 3584]) in TFLOP/s against the 2.5 PFLOP/s bf16 MFMA peak.
+
+    python bench.py [--gpus 1] [--steps 240] [--warmup 48]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _path in (REPO, os.path.join(REPO, "mini-llm-runtime_amd")):
+    if _path not in sys.path:
+        sys.path.insert(0, _path)
+
+METRIC = ("paged decode attn GB/s (% of HBM peak); "
+          "chunk-prefill attn TFLOP/s (% MFMA)")
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+LAYERS = 24
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=240)
+    p.add_argument("--warmup", type=int, default=48)
+    p.add_argument("--cpu-budget", type=float, default=20.0,
+                   help="seconds of CPU-baseline work (bounded sample)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--tokens-per-split", type=int, default=0)
+    return p.parse_args()
+
+
+def timed_graph(graph, replays, stream):
+    """Seconds for `replays` graph launches, bracketed by events on `stream`.
+
+    CUDAGraph.replay() launches on the current stream, so the replays run
+    inside `torch.cuda.stream(stream)`: events and kernels share one stream.
+    """
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3  # seconds
+
+
+def bench_decode(args, device):
+    import torch
+
+    from mini_llm_runtime_amd import _lib, workloads
+    from mini_llm_runtime_amd.kernels import paged_attention as kpa
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+
+    wl = workloads.bf16_decode_qwen05b_b64()
+    nb = wl.k_cache.shape[0]
+    cache = PagedKVCache(LAYERS, nb, 16, 2, 64, dtype=torch.bfloat16, device=device)
+    layer0_k, layer0_v = wl.k_cache.to(device), wl.v_cache.to(device)
+    for layer in range(LAYERS):
+        cache.k_cache[layer].copy_(layer0_k)
+        cache.v_cache[layer].copy_(layer0_v)
+    del layer0_k, layer0_v
+    q = wl.q.to(device)
+    bt = wl.block_tables.to(device)
+    ctx = wl.context_lens.to(device)
+    slots = wl.slot_mapping.to(device)
+    new_k, new_v = wl.new_k.to(device), wl.new_v.to(device)
+    out = torch.empty_like(q)
+    ts = args.tokens_per_split
+    ws_bytes = kpa.decode_workspace_bytes(64, 14, 64, bt.shape[1] * 16, torch.bfloat16, ts)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+
+    def step(layer, with_write=True):
+        if with_write:
+            cache._launch_write(slots, new_k, new_v, layer)
+        k_layer, v_layer = cache.get_layer_cache(layer)
+        kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out,
+                                tokens_per_split=ts, workspace=workspace)
+
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        for layer in range(LAYERS):   # eager warm-up: loads code objects
+            step(layer)
+    torch.cuda.current_stream(device).wait_stream(stream)
+    torch.cuda.synchronize()
+
+    graphs = {}
+    for name, with_write in (("step", True), ("decode", False)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for layer in range(LAYERS):
+                step(layer, with_write)
+        graphs[name] = g
+    torch.cuda.synchronize()
+
+    replays = max(1, -(-args.steps // LAYERS))
+    warm = max(1, -(-args.warmup // LAYERS))
+    for _ in range(warm):
+        graphs["step"].replay()
+        graphs["decode"].replay()
+    torch.cuda.synchronize()
+    t_step = timed_graph(graphs["step"], replays, stream)
+    t_decode = timed_graph(graphs["decode"], replays, stream)
+    steps = replays * LAYERS
+    decode_bytes = wl.algorithmic_bytes()
+    step_bytes = decode_bytes + wl.write_bytes()
+    sec_per_step = t_step / steps
+    sec_per_decode = t_decode / steps
+    return {
+        "wl": wl,
+        "steps": steps,
+        "warmup": warm * LAYERS,
+        "ms_per_step": sec_per_step * 1e3,
+        "value_gbs": step_bytes / sec_per_step / 1e9,
+        "decode_us": sec_per_decode * 1e6,
+        "decode_gbs": decode_bytes / sec_per_decode / 1e9,
+        "decode_bytes": decode_bytes,
+        "step_bytes": step_bytes,
+        "stream": stream,
+    }
+
+
+def bench_prefill(device, reps=20):
+    import torch
+
+    from mini_llm_runtime_amd import workloads
+    from mini_llm_runtime_amd.kernels import paged_attention as kpa
+
+    wl = workloads.bf16_prefill_chunk512_x8()
+    kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
+    kc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_k)
+    vc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_v)
+    kc, vc = kc.to(device), vc.to(device)
+    q = wl.q.to(device)
+    bt, qsl, ctx = (t.to(device) for t in (wl.block_tables, wl.query_start_loc,
+                                            wl.context_lens))
+    out = torch.empty_like(q)
+    results = {}
+    for tile in (16, 64, 128):
+        def call():
+            kpa.paged_prefill_launch(q, kc, vc, bt, qsl, ctx, 512, tile_size=tile, out=out)
+        stream = torch.cuda.Stream(device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            call()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            call()
+        g.replay()
+        secs = timed_graph(g, reps, stream) / reps
+        results[tile] = secs
+    best_tile = min(results, key=results.get)
+    flops = wl.causal_flops()
+    return {
+        "workload": "bf16_prefill_chunk512_x8",
+        "flops_per_call": flops,
+        "us_per_call": {str(t): round(s * 1e6, 2) for t, s in results.items()},
+        "best_tile": best_tile,
+        "tflops": flops / results[best_tile] / 1e12,
+        "wl": wl,
+    }
+
+
+def cpu_baseline_decode(wl, budget):
+    import torch
+
+    import oracle.paged_attention as opa
+    from oracle.paged_kv_cache import OracleKVCache
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cache = OracleKVCache(1, wl.k_cache.shape[0], 16, 2, 64, dtype=torch.bfloat16)
+    cache.k_cache[0].copy_(wl.k_cache)
+    cache.v_cache[0].copy_(wl.v_cache)
+
+    def step():
+        cache.write_slots(wl.slot_mapping, wl.new_k, wl.new_v, 0)
+        k_layer, v_layer = cache.get_layer_cache(0)
+        opa.decode_batch_parallel(wl.q, k_layer, v_layer, wl.block_tables,
+                                  wl.context_lens, 16)
+
+    step()  # warm-up
+    times, spent = [], 0.0
+    while len(times) < 5 or (spent < budget and len(times) < 50):
+        t0 = time.perf_counter()
+        step()
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        spent += dt
+        if spent > 3 * budget:
+            break
+    med = statistics.median(times)
+    return {
+        "value": (wl.algorithmic_bytes() + wl.write_bytes()) / med / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"full bf16_decode_qwen05b_b64 step (64-token write_slots + "
+                   f"decode_batch_parallel, oracle restatement in PyTorch CPU), "
+                   f"median of {len(times)} runs after 1 warm-up, "
+                   f"{med * 1e3:.1f} ms/step"),
+    }
+
+
+def cpu_baseline_prefill(wl, budget):
+    import torch
+
+    import oracle.paged_attention as opa
+
+    kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
+    kc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_k)
+    vc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_v)
+    flops, spent, seqs = 0, 0.0, 0
+    for s in range(len(wl.prefix_lens)):
+        lo, hi = int(wl.query_start_loc[s]), int(wl.query_start_loc[s + 1])
+        p = wl.prefix_lens[s]
+        t0 = time.perf_counter()
+        opa.prefill_chunk_tiled(wl.q[lo:hi], kc, vc, wl.tables[s], p, p + hi - lo, 16, 64)
+        spent += time.perf_counter() - t0
+        flops += 4 * 64 * 14 * ((hi - lo) * p + (hi - lo) * (hi - lo + 1) // 2)
+        seqs += 1
+        if spent > budget:
+            break
+    return {
+        "value": flops / spent / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{seqs} of 8 sequences of bf16_prefill_chunk512_x8 "
+                  f"(prefill_chunk_tiled, tile 64), {spent:.1f} s",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the paged attention path has no cross-GPU "
+              "step in this build (see DESIGN.md, 'How the path would shard'); "
+              "run it with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    device = torch.device("cuda", 0)
+    dec = bench_decode(args, device)
+    pre = None if args.no_prefill else bench_prefill(device)
+    cpu = None
+    cpu_pre = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_decode(dec["wl"], args.cpu_budget)
+        if pre is not None:
+            cpu_pre = cpu_baseline_prefill(pre["wl"], args.cpu_budget / 2)
+    line = {
+        "metric": METRIC,
+        "value": round(dec["value_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": dec["steps"],
+        "warmup": dec["warmup"],
+        "ms_per_step": round(dec["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "bf16_decode_qwen05b_b64",
+            "batch": 64, "num_q_heads": 14, "num_kv_heads": 2, "head_dim": 64,
+            "block_size": 16, "context": "U[128,4096]", "num_blocks": 24576,
+            "kv_write_tokens": 64, "layers_rotated": LAYERS,
+            "step": "kv write + split-KV decode (split + combine), one layer",
+            "step_bytes": dec["step_bytes"],
+            "hbm_pct_of_peak": round(100 * dec["value_gbs"] / HBM_PEAK_GBS, 2),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mlr_paged_decode (decode_split_mfma<64> + decode_combine)",
+            "achieved": round(dec["decode_gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec["decode_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": dec["decode_bytes"],
+            "avg_launch_us": round(dec["decode_us"], 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    if pre is not None:
+        line["prefill"] = {
+            "workload": pre["workload"],
+            "value": round(pre["tflops"], 3),
+            "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 3),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 5),
+                         "traffic": None},
+            "flops_per_call": pre["flops_per_call"],
+            "us_per_call_by_kv_tile": pre["us_per_call"],
+            "cpu_baseline": cpu_pre,
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -60,19 +60,26 @@ __global__ __launch_bounds__(256) void kv_write_vec16_kernel(
     const void *__restrict__ slots, uint4 *__restrict__ kc,
     uint4 *__restrict__ vc, int64_t num_slots, int64_t hkv,
     int64_t chunks_per_row) {
-  // Strides here are in 16-byte chunks.
-  const int64_t n = num_tokens * hkv * chunks_per_row;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t c = i % chunks_per_row;
-    const int64_t r = i / chunks_per_row;
-    const int64_t h = r % hkv;
-    const int64_t t = r / hkv;
+  // Strides here are in 16-byte chunks. The host launches this kernel only
+  // when num_tokens * hkv * chunks_per_row fits 32 bits.
+  const uint32_t n = static_cast<uint32_t>(num_tokens * hkv * chunks_per_row);
+  const uint32_t cpr = static_cast<uint32_t>(chunks_per_row);
+  const uint32_t nh = static_cast<uint32_t>(hkv);
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += gridDim.x * blockDim.x) {
+    const uint32_t c = i % cpr;
+    const uint32_t r = i / cpr;
+    const uint32_t h = r % nh;
+    const uint32_t t = r / nh;
+    // The source rows do not depend on the slot: all three loads are in
+    // flight together.
+    const uint4 kv = k[t * kst + h * ksh + c];
+    const uint4 vv = v[t * vst + h * vsh + c];
     const int64_t slot = load_slot<I>(slots, t);
     if (slot < 0 || slot >= num_slots) continue;
     const int64_t dst = (slot * hkv + h) * chunks_per_row + c;
-    kc[dst] = k[t * kst + h * ksh + c];
-    vc[dst] = v[t * vst + h * vsh + c];
+    kc[dst] = kv;
+    vc[dst] = vv;
   }
 }
 
@@ -177,7 +184,8 @@ extern "C" int mlr_kv_write(const void *k, const void *v, int src_dtype,
       (k_stride_h % elems_per_chunk) == 0 &&
       (v_stride_t % elems_per_chunk) == 0 &&
       (v_stride_h % elems_per_chunk) == 0 && aligned16(k) && aligned16(v) &&
-      aligned16(k_cache) && aligned16(v_cache);
+      aligned16(k_cache) && aligned16(v_cache) &&
+      num_tokens * num_kv_heads * (row_bytes / 16) < (int64_t(1) << 31);
   if (vec_ok) {
     const int64_t cpr = row_bytes / 16;
     const int64_t n = num_tokens * num_kv_heads * cpr;

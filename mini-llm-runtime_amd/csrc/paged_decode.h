@@ -25,8 +25,9 @@ struct DecodeParams {
   double scale;
   int ts;          // tokens per split
   int max_splits;  // splits covering max_blocks * block_size tokens
-  float2 *ws_ml;   // [batch][hq][max_splits] = (m in natural-log units, l)
+  float2 *ws_ml;   // [batch][hq][max_splits] = (m, l)
   void *ws_acc;    // [batch][hq][max_splits][d], FP32 (FP64 for f64 inputs)
+  int ml_base2;    // 1: m is a base-2 exponent, 0: natural-log units
   void *out;
   int64_t o_sb, o_sh;
 };

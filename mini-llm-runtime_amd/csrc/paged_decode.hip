@@ -162,7 +162,9 @@ __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
   float l = 0.f;
   for (int s = threadIdx.x; s < ns; s += blockDim.x) {
     const float2 v = ml[s];
-    const float w = (v.x == -INFINITY) ? 0.f : expf(v.x - M);
+    const float w = (v.x == -INFINITY) ? 0.f
+                    : p.ml_base2      ? exp2f(v.x - M)
+                                      : expf(v.x - M);
     w_s[s] = w;
     l += w * v.y;
   }
@@ -214,9 +216,10 @@ int launch_combine(const DecodeParams &p, hipStream_t stream) {
 template int launch_combine<bf16_t>(const DecodeParams &, hipStream_t);
 
 int64_t default_tokens_per_split(int dtype, int64_t head_dim) {
-  // The bf16 MFMA kernel streams tiles, so longer splits only cost parallelism;
-  // the generic kernel holds a split's scores in LDS (<= kGenMaxSplit).
-  if (dtype == MLR_DTYPE_BF16 && (head_dim == 64 || head_dim == 128)) return 512;
+  // 256 tokens = 16 tiles: four per wave of the MFMA kernel, which loads them
+  // in one batch; the generic kernel holds a split's scores in LDS.
+  (void)dtype;
+  (void)head_dim;
   return 256;
 }
 
@@ -338,6 +341,7 @@ extern "C" int mlr_paged_decode(
   p.max_splits = static_cast<int>(max_splits);
   p.ws_ml = static_cast<float2 *>(workspace);
   p.ws_acc = static_cast<unsigned char *>(workspace) + wl.acc_offset;
+  p.ml_base2 = mfma ? 1 : 0;
   p.out = out;
   p.o_sb = out_stride_b;
   p.o_sh = out_stride_h;

@@ -1,4 +1,4 @@
-// bf16 split-KV paged decode on gfx950 matrix cores (pass 1).
+// bf16 split-KV paged decode on gfx950 matrix cores.
 //
 // One workgroup of four wavefronts per (sequence, KV head, split). The split's
 // 16-token tiles are dealt round-robin to the four waves; each wave keeps the
@@ -19,8 +19,14 @@
 //       lanes covers a whole 128/256-byte row, and a 4x4 transpose of 16-bit
 //       halves inside the lane builds the A operand: tile n, row m <-> dim
 //       (D/16)*m + n.
-// The four waves then merge through LDS and write (m, l, acc) for the split,
-// which the combine kernel (paged_decode.hip) folds into the output.
+// Memory-level parallelism: a wave issues the loads of a whole batch of
+// kBatch tiles at once and the next batch's loads before computing the
+// current one (two register buffers), so 8-16 KiB per wave are in flight.
+//
+// The four waves merge through LDS. A sequence that fits one split writes its
+// output directly; otherwise each workgroup stores its split's (m, l, acc) and
+// the combine kernel merges the splits of each (sequence, KV head):
+//   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s.
 //
 // Scores are rounded like the reference's bf16 matmul (to bf16, times scale,
 // to bf16 again: kernels/reference/paged_attention.py:246-247) before the
@@ -36,7 +42,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
 
 template <int D> struct VRow;
 template <> struct VRow<64> { using type = uint2; };   // 4 bf16 per lane
@@ -69,204 +74,332 @@ __device__ __forceinline__ uint32_t vword(const typename VRow<D>::type &v, int c
   }
 }
 
+// Registers of one loaded tile. blk and rel are wave-uniform.
 template <int D>
-__global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
-  constexpr int QK = D / 32;  // 16x16x32 steps for S^T
-  constexpr int VC = D / 16;  // PV tiles = dims per lane per V row
-  using VT = typename VRow<D>::type;
+struct Tile {
+  uint4 k[D / 32];
+  typename VRow<D>::type v[4];
+  int blk;  // physical block id, -1 when the tile is absent or invalid
+  int rel;  // position of the tile's first token relative to the split start
+};
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+template <int D>
+struct DecodeState {
+  f32x4_t acc[D / 16];
+  float m, l;
+};
+
+// Per-lane byte offsets inside a 16-token tile, fixed for the whole kernel.
+struct LaneOffsets {
+  int k;       // K row of token m16, dims 8g..: ((m16 * hkv + kvh) * D + 8g) * 2
+  int v;       // V row of token 4g, dims VC*m16..: ((4g * hkv + kvh) * D + VC*m16) * 2
+  int v_step;  // bytes between consecutive token rows (hkv * D * 2)
+};
+
+// Raw buffer resource over one physical block (gfx9 descriptor word 3). The
+// base is wave-uniform, so the loads use a scalar descriptor plus 32-bit lane
+// offsets, and the hardware drops any access outside the block.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const uint16_t *base,
+                                                             uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes,
+                                           0x00020000);
+}
+
+template <int D>
+__device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
+                                          const uint16_t *vc, int64_t block_elems,
+                                          int tile_off_bytes, int blk, int rel,
+                                          const LaneOffsets &o) {
+  constexpr int QK = D / 32;
+  using VT = typename VRow<D>::type;
+  t.blk = blk;
+  t.rel = rel;
+  if (blk >= 0) {
+    const uint32_t bytes = static_cast<uint32_t>(block_elems * 2);
+    const __amdgpu_buffer_rsrc_t rk = block_rsrc(kc + (int64_t)blk * block_elems, bytes);
+    const __amdgpu_buffer_rsrc_t rv = block_rsrc(vc + (int64_t)blk * block_elems, bytes);
+#pragma unroll
+    for (int j = 0; j < QK; ++j)
+      t.k[j] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, o.k + 64 * j, tile_off_bytes, 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (D == 64) {
+        t.v[i] = __builtin_bit_cast(
+            VT, __builtin_amdgcn_raw_buffer_load_b64(rv, o.v + i * o.v_step, tile_off_bytes, 0));
+      } else {
+        t.v[i] = __builtin_bit_cast(
+            VT, __builtin_amdgcn_raw_buffer_load_b128(rv, o.v + i * o.v_step, tile_off_bytes, 0));
+      }
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
+                                             const bf16x8_t *qf, float scale,
+                                             int live, int g) {
+  constexpr int QK = D / 32, VC = D / 16;
+  using VT = typename VRow<D>::type;
+  if (t.blk < 0) return;  // absent tile or invalid block id: no keys (uniform)
+  const int lim = live - t.rel;  // tokens of this tile inside the context
+
+  f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < QK; ++j)
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, t.k[j]),
+                                                qf[j], s, 0, 0, 0);
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float r = bf16_round(bf16_round(s[i]) * scale);
+    x[i] = (4 * g + i < lim) ? r * kLog2e : -INFINITY;
+  }
+  float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float m_new = fmaxf(st.m, mx);  // finite: every tile has a live token
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  float pr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+  st.l = st.l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+  st.m = m_new;
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int n = 0; n < VC; ++n) st.acc[n] *= alpha;
+  }
+  // Tokens past the context may hold anything (even NaN): zero their V.
+  if (lim < 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * g + i >= lim) t.v[i] = VT{};
+  }
+  const s16x4_t pb = __builtin_bit_cast(
+      s16x4_t, make_uint2(bf16_pack2(pr[0], pr[1]), bf16_pack2(pr[2], pr[3])));
+#pragma unroll
+  for (int n = 0; n < VC; ++n) {
+    const int c = n >> 1, h = n & 1;
+    const uint32_t lo = half16(vword<D>(t.v[0], c), h) | (half16(vword<D>(t.v[1], c), h) << 16);
+    const uint32_t hi = half16(vword<D>(t.v[2], c), h) | (half16(vword<D>(t.v[3], c), h) << 16);
+    const s16x4_t va = __builtin_bit_cast(s16x4_t, make_uint2(lo, hi));
+    st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, st.acc[n], 0, 0, 0);
+  }
+}
+
+template <int D, int kBatch, bool kDouble>
+__global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
+  constexpr int QK = D / 32;
+  constexpr int VC = D / 16;
+
+  // Grid (batch, KV head, split): split is the slowest dimension, so the
+  // dispatcher hands out every sequence's first split before any later one
+  // and the workgroups of splits past short contexts (which exit at once)
+  // come last.
+  const int b = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  // The wave index is uniform within a wave; saying so keeps every value
+  // derived from it (tile counts, block ids, descriptors) in SGPRs.
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m16 = lane & 15, g = lane >> 4;
 
-  const int64_t cap = p.max_blocks * p.block_size;
-  int64_t ctx = p.ctx[b];
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int64_t t0 = static_cast<int64_t>(split) * p.ts;
-  if (t0 >= ctx) return;  // uniform over the workgroup
-  const int64_t t1 = min<int64_t>(ctx, t0 + p.ts);
-  const int ntiles = static_cast<int>(ceil_div(t1 - t0, 16));
+  const int64_t *bt_row = p.bt + b * p.bt_stride;
 
-  // Q^T as the B operand: lane l holds Q[head l%16][32j + 8g .. +8).
+  // Prologue: the context length, the Q fragments and the first 64 block ids
+  // of this wave do not depend on one another, so all three loads are issued
+  // before any is used (one memory latency). Block ids are read for every
+  // tile position the split could hold, within the table's width.
+  const int64_t ctx_raw = p.ctx[b];
   const bool head_ok = m16 < p.group;
   const uint16_t *qrow = static_cast<const uint16_t *>(p.q) + b * p.q_sb +
                          (int64_t)(kvh * p.group + (head_ok ? m16 : 0)) * p.q_sh;
+  uint4 qraw[QK];
+#pragma unroll
+  for (int j = 0; j < QK; ++j)
+    qraw[j] = head_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * j + 8 * g)
+                      : make_uint4(0, 0, 0, 0);
+  auto raw_block_id = [&](int k) -> int64_t {
+    const int64_t idx = (t0 + 16LL * (w + kWaves * k)) / p.block_size;
+    return idx < p.max_blocks ? bt_row[idx] : int64_t(-1);
+  };
+  int64_t blk_raw = raw_block_id(lane);
+
+  const int64_t cap = p.max_blocks * p.block_size;
+  const int64_t ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
+  if (t0 >= ctx) return;  // uniform over the workgroup
+  const int64_t t1 = min<int64_t>(ctx, t0 + p.ts);
+  const int ntiles = static_cast<int>(ceil_div(t1 - t0, 16));
+  const int nsplits = static_cast<int>(ceil_div(ctx, p.ts));
+
+  // Q^T as the B operand: lane l holds Q[head l%16][32j + 8g .. +8).
   bf16x8_t qf[QK];
 #pragma unroll
-  for (int j = 0; j < QK; ++j) {
-    uint4 raw = head_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * j + 8 * g)
-                        : make_uint4(0, 0, 0, 0);
-    qf[j] = __builtin_bit_cast(bf16x8_t, raw);
-  }
+  for (int j = 0; j < QK; ++j) qf[j] = __builtin_bit_cast(bf16x8_t, qraw[j]);
 
   const uint16_t *kc = static_cast<const uint16_t *>(p.kc);
   const uint16_t *vc = static_cast<const uint16_t *>(p.vc);
-  const int64_t row_stride = (int64_t)p.hkv * D;  // elements between slots
-  const int64_t *bt_row = p.bt + b * p.bt_stride;
   const float scale = static_cast<float>(p.scale);
 
-  f32x4_t acc[VC];
+  DecodeState<D> st;
 #pragma unroll
-  for (int n = 0; n < VC; ++n) acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int n = 0; n < VC; ++n) st.acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.f;
 
-  // This wave's tiles: w, w + 4, w + 8, ...
+  // This wave's tiles: w, w + 4, w + 8, ...; block id of the wave's k-th
+  // tile lives in lane (k % 64) of blk_reg (-1: no tile or invalid id).
   const int nk = ntiles > w ? (ntiles - w + kWaves - 1) / kWaves : 0;
-
-  // Block id of the wave's k-th tile lives in lane (k % 64) of blk_reg.
-  int blk_reg = -1;
+  auto valid_id = [&](int k, int64_t raw) -> int {
+    return (k < nk && raw >= 0 && raw < p.num_blocks) ? static_cast<int>(raw) : -1;
+  };
+  int blk_reg = valid_id(lane, blk_raw);
   auto load_block_ids = [&](int kbase) {
+    if (kbase == 0) return;  // the prologue loaded the first 64
     const int k = kbase + lane;
-    int id = -1;
-    if (k < nk) {
-      const int64_t pos = t0 + 16LL * (w + kWaves * k);
-      const int64_t blk = bt_row[pos / p.block_size];
-      id = (blk >= 0 && blk < p.num_blocks) ? static_cast<int>(blk) : -1;
+    blk_reg = valid_id(k, k < nk ? raw_block_id(k) : int64_t(-1));
+  };
+  const int row_elems = p.hkv * D;  // elements of one slot (token row)
+  const int64_t block_elems = p.block_size * row_elems;
+  LaneOffsets lo;
+  lo.k = ((m16 * p.hkv + kvh) * D + 8 * g) * 2;
+  lo.v = ((4 * g * p.hkv + kvh) * D + VC * m16) * 2;
+  lo.v_step = row_elems * 2;
+  const int live = static_cast<int>(t1 - t0);
+  auto issue = [&](Tile<D>(&buf)[kBatch], int kb) {
+    if ((kb & 63) == 0) load_block_ids(kb);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int k = kb + u;
+      const int blk = k < nk ? __builtin_amdgcn_readlane(blk_reg, k & 63) : -1;
+      const int rel = 16 * (w + kWaves * k);
+      // Byte offset of the tile's first token inside its block.
+      const int tile_off = static_cast<int>((t0 + rel) % p.block_size) * row_elems * 2;
+      load_tile<D>(buf[u], kc, vc, block_elems, tile_off, blk, rel, lo);
     }
-    blk_reg = id;
+  };
+  auto compute = [&](Tile<D>(&buf)[kBatch]) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) compute_tile<D>(st, buf[u], qf, scale, live, g);
   };
 
-  uint4 kcur[QK], knext[QK];
-  VT vcur[4], vnext[4];
-  auto load_tile = [&](int k, uint4 *kr, VT *vr) {
-    const int blk = __builtin_amdgcn_readlane(blk_reg, k & 63);
-    const int64_t pos = t0 + 16LL * (w + kWaves * k);
-    if (blk >= 0) {
-      const int64_t slot0 = (int64_t)blk * p.block_size + pos % p.block_size;
-      const uint16_t *kb = kc + (slot0 + m16) * row_stride + (int64_t)kvh * D;
-#pragma unroll
-      for (int j = 0; j < QK; ++j)
-        kr[j] = *reinterpret_cast<const uint4 *>(kb + 32 * j + 8 * g);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint16_t *vb =
-            vc + (slot0 + 4 * g + i) * row_stride + (int64_t)kvh * D + VC * m16;
-        vr[i] = *reinterpret_cast<const VT *>(vb);
+  if constexpr (kDouble) {
+    // Next batch in flight while the current one computes.
+    if (nk > 0) {
+      Tile<D> bufA[kBatch], bufB[kBatch];
+      issue(bufA, 0);
+      for (int kb = 0; kb < nk; kb += 2 * kBatch) {
+        if (kb + kBatch < nk) issue(bufB, kb + kBatch);
+        compute(bufA);
+        if (kb + kBatch >= nk) break;
+        if (kb + 2 * kBatch < nk) issue(bufA, kb + 2 * kBatch);
+        compute(bufB);
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < QK; ++j) kr[j] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vr[i] = VT{};
     }
-  };
-
-  if (nk > 0) {
-    load_block_ids(0);
-    load_tile(0, kcur, vcur);
-  }
-  for (int k = 0; k < nk; ++k) {
-    // Read this tile's block id before the next chunk of ids replaces it.
-    const int blk = __builtin_amdgcn_readlane(blk_reg, k & 63);
-    const int64_t base = t0 + 16LL * (w + kWaves * k);
-    if (k + 1 < nk) {
-      if (((k + 1) & 63) == 0) load_block_ids(k + 1);
-      load_tile(k + 1, knext, vnext);
-    }
-
-    // S^T = K . Q^T
-    f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < QK; ++j)
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          __builtin_bit_cast(bf16x8_t, kcur[j]), qf[j], s, 0, 0, 0);
-
-    // Reference rounding, masking past the context, base-2 scaling.
-    float x[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float r = bf16_round(bf16_round(s[i]) * scale);
-      const bool live = blk >= 0 && base + 4 * g + i < t1;
-      x[i] = live ? r * kLog2e : -INFINITY;
-    }
-    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const bool any = m_new != -INFINITY;
-    const float alpha = any ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      pr[i] = any ? __builtin_amdgcn_exp2f(x[i] - m_new) : 0.f;
-    l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    m_run = m_new;
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int n = 0; n < VC; ++n) acc[n] *= alpha;
-    }
-
-    // Tokens past the context may hold anything (even NaN): zero their V.
-    if (base + 16 > t1) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (base + 4 * g + i >= t1) vcur[i] = VT{};
-    }
-
-    s16x4_t pb;
-    {
-      const uint32_t lo = bf16_pack2(pr[0], pr[1]);
-      const uint32_t hi = bf16_pack2(pr[2], pr[3]);
-      pb = __builtin_bit_cast(s16x4_t, make_uint2(lo, hi));
-    }
-#pragma unroll
-    for (int n = 0; n < VC; ++n) {
-      const int c = n >> 1, h = n & 1;
-      const uint32_t lo = half16(vword<D>(vcur[0], c), h) |
-                          (half16(vword<D>(vcur[1], c), h) << 16);
-      const uint32_t hi = half16(vword<D>(vcur[2], c), h) |
-                          (half16(vword<D>(vcur[3], c), h) << 16);
-      const s16x4_t va = __builtin_bit_cast(s16x4_t, make_uint2(lo, hi));
-      acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[n], 0, 0, 0);
-    }
-
-    if (k + 1 < nk) {
-#pragma unroll
-      for (int j = 0; j < QK; ++j) kcur[j] = knext[j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vcur[i] = vnext[i];
+  } else {
+    Tile<D> buf[kBatch];
+    for (int kb = 0; kb < nk; kb += kBatch) {
+      issue(buf, kb);
+      compute(buf);
     }
   }
 
   // Per-head l: sum the four lanes that share the head.
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
+  st.l += __shfl_xor(st.l, 16);
+  st.l += __shfl_xor(st.l, 32);
 
   __shared__ float o_s[kWaves][16][D + 4];
   __shared__ float m_s[kWaves][16];
   __shared__ float l_s[kWaves][16];
   if (g == 0) {
-    m_s[w][m16] = m_run;
-    l_s[w][m16] = l_run;
+    m_s[w][m16] = st.m;
+    l_s[w][m16] = st.l;
   }
-  // Lane l holds O[head l%16][dims VC*(4g+i) + n] = a contiguous 4*VC run.
+  // Lane l holds O[head l%16][dims VC*(4g+i) + n].
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int n = 0; n < VC; ++n) o_s[w][m16][VC * (4 * g + i) + n] = acc[n][i];
+    for (int n = 0; n < VC; ++n) o_s[w][m16][VC * (4 * g + i) + n] = st.acc[n][i];
   }
   __syncthreads();
 
-  float *ws_acc = static_cast<float *>(p.ws_acc);
+  // Merge the four waves. A sequence that fits one split is finished here;
+  // otherwise the split's (m, l, acc) go to the workspace for the combine
+  // kernel (m as a base-2 exponent).
   const int head0 = kvh * p.group;
+  uint16_t *out = static_cast<uint16_t *>(p.out);
+  float *ws_acc = static_cast<float *>(p.ws_acc);
   for (int idx = threadIdx.x; idx < p.group * D; idx += blockDim.x) {
     const int h = idx / D, d = idx % D;
     float M = m_s[0][h];
 #pragma unroll
     for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, m_s[ww][h]);
     float num = 0.f, den = 0.f;
-    if (M != -INFINITY) {
 #pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) {
-        const float f = __builtin_amdgcn_exp2f(m_s[ww][h] - M);
-        num += f * o_s[ww][h][d];
-        den += f * l_s[ww][h];
-      }
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float f = __builtin_amdgcn_exp2f(m_s[ww][h] - M);
+      num += f * o_s[ww][h][d];
+      den += f * l_s[ww][h];
     }
-    const int64_t row = ((int64_t)b * p.hq + head0 + h) * p.max_splits + split;
-    ws_acc[row * D + d] = num;
-    if (d == 0) p.ws_ml[row] = make_float2(M == -INFINITY ? M : M * kLn2, den);
+    if (nsplits == 1) {
+      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num / den);
+    } else {
+      const int64_t row = ((int64_t)b * p.hq + head0 + h) * p.max_splits + split;
+      ws_acc[row * D + d] = num;
+      if (d == 0) p.ws_ml[row] = make_float2(M, den);
+    }
   }
+}
+
+// Pass 2 for the bf16 kernel: one wave per (query head, sequence) merges the
+// splits; sequences with one split are already done. Splits go in chunks of
+// kChunk: the chunk's (m, l) (lane s holds split s) and acc rows (lane d holds
+// dims d, d+64) are all loaded before any arithmetic, so a chunk costs one
+// memory latency; chunks after the first rescale the running sums.
+template <int D>
+__global__ __launch_bounds__(64) void decode_combine_mfma(DecodeParams p) {
+  constexpr int kChunk = 16;
+  constexpr int C = D / 64;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t cap = p.max_blocks * p.block_size;
+  int64_t ctx = p.ctx[b];
+  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int ns = static_cast<int>(ceil_div(ctx, p.ts));
+  if (ns <= 1) return;
+  const float *ws_acc = static_cast<const float *>(p.ws_acc);
+  const int64_t row0 = ((int64_t)b * p.hq + h) * p.max_splits;
+  float num[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) num[c] = 0.f;
+  float den = 0.f, M = -INFINITY;
+  for (int s0 = 0; s0 < ns; s0 += kChunk) {
+    const int cnt = min(kChunk, ns - s0);
+    float a[kChunk][C];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        a[j][c] = j < cnt ? ws_acc[(row0 + s0 + j) * D + 64 * c + lane] : 0.f;
+    }
+    const float2 ml = lane < cnt ? p.ws_ml[row0 + s0 + lane] : make_float2(-INFINITY, 0.f);
+    const float m_new = fmaxf(M, wave_max(ml.x));
+    const float rescale = __builtin_amdgcn_exp2f(M - m_new);  // 0 on the first chunk
+    const float f = __builtin_amdgcn_exp2f(ml.x - m_new);
+    den = den * rescale + wave_sum(f * ml.y);
+    M = m_new;
+#pragma unroll
+    for (int c = 0; c < C; ++c) num[c] *= rescale;
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const float fj = __shfl(f, j);
+#pragma unroll
+      for (int c = 0; c < C; ++c) num[c] += fj * a[j][c];
+    }
+  }
+  uint16_t *out = static_cast<uint16_t *>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
+#pragma unroll
+  for (int c = 0; c < C; ++c) out[64 * c + lane] = float_to_bf16_bits(num[c] / den);
 }
 
 }  // namespace
@@ -278,15 +411,31 @@ bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
 }
 
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
-  dim3 grid(p.max_splits, p.hkv, p.batch);
+  dim3 grid(p.batch, p.hkv, p.max_splits);
+  // Tiles per wave: ceil(ts / 16 / 4). A split whose tiles fit one load batch
+  // needs no second register buffer (fewer VGPRs, more waves per SIMD).
+  const int tiles_per_wave = static_cast<int>(ceil_div(ceil_div(p.ts, 16), kWaves));
   if (p.d == 64) {
-    decode_split_mfma<64><<<grid, 256, 0, stream>>>(p);
+    if (tiles_per_wave <= 4)
+      decode_split_mfma<64, 4, false><<<grid, 256, 0, stream>>>(p);
+    else
+      decode_split_mfma<64, 4, true><<<grid, 256, 0, stream>>>(p);
   } else {
-    decode_split_mfma<128><<<grid, 256, 0, stream>>>(p);
+    if (tiles_per_wave <= 2)
+      decode_split_mfma<128, 2, false><<<grid, 256, 0, stream>>>(p);
+    else
+      decode_split_mfma<128, 2, true><<<grid, 256, 0, stream>>>(p);
   }
   int rc = check_launch("mlr_paged_decode(split, mfma)");
   if (rc != MLR_OK) return rc;
-  return launch_combine<bf16_t>(p, stream);
+  if (p.max_splits <= 1) return MLR_OK;  // every sequence fits one split
+  dim3 cgrid(p.hq, p.batch);
+  if (p.d == 64) {
+    decode_combine_mfma<64><<<cgrid, 64, 0, stream>>>(p);
+  } else {
+    decode_combine_mfma<128><<<cgrid, 64, 0, stream>>>(p);
+  }
+  return check_launch("mlr_paged_decode(combine, mfma)");
 }
 
 }  // namespace mlr

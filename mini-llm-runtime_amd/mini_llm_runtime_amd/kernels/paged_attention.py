@@ -96,6 +96,7 @@ def paged_decode_launch(q: torch.Tensor, k_cache: torch.Tensor,
         batch, num_q_heads, head_dim, width * block_size, tokens_per_split, dcode))
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
+    stream = _lib.stream_handle(device)
     with torch.cuda.device(device):
         status = lib.mlr_paged_decode(
             q.data_ptr(), q.stride(0), q.stride(1),
@@ -105,7 +106,7 @@ def paged_decode_launch(q: torch.Tensor, k_cache: torch.Tensor,
             seq_lens.data_ptr(), batch, num_q_heads, float(scale), dcode,
             int(tokens_per_split), workspace.data_ptr(), workspace.numel(),
             out.data_ptr(), out.stride(0), out.stride(1),
-            _lib.stream_handle(device))
+            stream)
     _lib.check(status, "mlr_paged_decode")
     return out
 
