@@ -124,6 +124,33 @@ int mlr_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                      int64_t out_stride_h, void *stream);
 
 /*
+ * One decode step with the KV write folded in: for every sequence b, the new
+ * token's rows new_k[b], new_v[b] ([batch, num_kv_heads, head_dim] in the cache
+ * dtype, strides (new_stride_b, new_stride_h), unit stride along head_dim) are
+ * written to slot slot_mapping[b] of k_cache/v_cache and attended to as the
+ * token at position context_lens[b] - 1. Cache contents and output equal
+ * mlr_kv_write(new_k, new_v, slot_mapping) followed by mlr_paged_decode(...)
+ * when, as the reference requires of a decode step, slot_mapping[b] is the slot
+ * of position context_lens[b] - 1 and the slots are distinct
+ * (model/qwen2.py:595-602). The bf16 kernel writes the rows and uses them from
+ * registers, saving the separate write kernel; other dtypes run the two
+ * kernels in sequence.
+ *
+ * Replaces the write_slots + paged_attention_decode_batch_parallel pair of
+ * Qwen2Attention.forward_decode_batch_with_cache (model/qwen2.py:608-621).
+ */
+int mlr_paged_decode_append(
+    const void *q, int64_t q_stride_b, int64_t q_stride_h, void *k_cache,
+    void *v_cache, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+    int64_t head_dim, const int64_t *block_tables, int64_t block_table_stride,
+    int64_t max_blocks_per_seq, const int64_t *context_lens, int64_t batch,
+    int64_t num_q_heads, double scale, int dtype, int64_t tokens_per_split,
+    void *workspace, size_t workspace_bytes, const void *new_k,
+    const void *new_v, int64_t new_stride_b, int64_t new_stride_h,
+    const int64_t *slot_mapping, void *out, int64_t out_stride_b,
+    int64_t out_stride_h, void *stream);
+
+/*
  * Paged chunk-prefill attention for a packed batch of sequences (varlen):
  * sequence s owns query rows [query_start_loc[s], query_start_loc[s+1]) of q,
  * whose absolute positions are prefix_len_s + i with

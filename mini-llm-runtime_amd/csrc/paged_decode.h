@@ -30,6 +30,13 @@ struct DecodeParams {
   int ml_base2;    // 1: m is a base-2 exponent, 0: natural-log units
   void *out;
   int64_t o_sb, o_sh;
+  // Fused KV write (mlr_paged_decode_append); new_k == nullptr: none.
+  const void *new_k;
+  const void *new_v;
+  int64_t new_sb, new_sh;
+  const int64_t *new_slots;
+  void *kc_w;  // writable views of kc / vc
+  void *vc_w;
 };
 
 struct DecodeWorkspace {

@@ -254,16 +254,25 @@ extern "C" size_t mlr_paged_decode_workspace_size(int64_t batch,
       decode_workspace_layout(batch, num_q_heads, head_dim, splits, dtype).total);
 }
 
-extern "C" int mlr_paged_decode(
-    const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *k_cache,
-    const void *v_cache, int64_t num_blocks, int64_t block_size,
-    int64_t num_kv_heads, int64_t head_dim, const int64_t *block_tables,
-    int64_t block_table_stride, int64_t max_blocks_per_seq,
-    const int64_t *context_lens, int64_t batch, int64_t num_q_heads,
-    double scale, int dtype, int64_t tokens_per_split, void *workspace,
-    size_t workspace_bytes, void *out, int64_t out_stride_b,
-    int64_t out_stride_h, void *stream) {
-  clear_error();
+namespace {
+
+// The new-token rows of mlr_paged_decode_append.
+struct AppendArgs {
+  const void *new_k;
+  const void *new_v;
+  int64_t sb, sh;
+  const int64_t *slots;
+};
+
+int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+               const void *k_cache, const void *v_cache, int64_t num_blocks,
+               int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+               const int64_t *block_tables, int64_t block_table_stride,
+               int64_t max_blocks_per_seq, const int64_t *context_lens,
+               int64_t batch, int64_t num_q_heads, double scale, int dtype,
+               int64_t tokens_per_split, void *workspace,
+               size_t workspace_bytes, void *out, int64_t out_stride_b,
+               int64_t out_stride_h, void *stream, const AppendArgs *app) {
   MLR_REQUIRE(batch > 0, "mlr_paged_decode: batch must be > 0");
   MLR_REQUIRE(num_kv_heads > 0 && num_q_heads > 0,
               "mlr_paged_decode: head counts must be > 0");
@@ -347,6 +356,31 @@ extern "C" int mlr_paged_decode(
   p.o_sh = out_stride_h;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (app != nullptr) {
+    MLR_REQUIRE(app->new_k && app->new_v && app->slots,
+                "mlr_paged_decode_append: null new_k, new_v or slot_mapping");
+    // The MFMA kernel moves 16-byte K and 8/16-byte V fragments of the rows.
+    const bool rows_aligned = (reinterpret_cast<uintptr_t>(app->new_k) & 15u) == 0 &&
+                              (reinterpret_cast<uintptr_t>(app->new_v) & 15u) == 0 &&
+                              app->sb % 8 == 0 && app->sh % 8 == 0;
+    if (mfma && rows_aligned) {
+      p.new_k = app->new_k;
+      p.new_v = app->new_v;
+      p.new_sb = app->sb;
+      p.new_sh = app->sh;
+      p.new_slots = app->slots;
+      p.kc_w = const_cast<void *>(k_cache);
+      p.vc_w = const_cast<void *>(v_cache);
+    } else {
+      const int rc = mlr_kv_write(app->new_k, app->new_v, dtype, batch, app->sb,
+                                  app->sh, 1, app->sb, app->sh, 1, app->slots,
+                                  MLR_INDEX_I64, const_cast<void *>(k_cache),
+                                  const_cast<void *>(v_cache), dtype,
+                                  num_blocks * block_size, num_kv_heads, head_dim,
+                                  stream);
+      if (rc != MLR_OK) return rc;
+    }
+  }
   if (mfma) return launch_decode_mfma(p, s);
   switch (dtype) {
     case MLR_DTYPE_F32: return launch_generic<float>(p, s);
@@ -355,4 +389,44 @@ extern "C" int mlr_paged_decode(
     case MLR_DTYPE_F64: return launch_generic<double>(p, s);
     default: return set_error(MLR_ERR_INVALID, "mlr_paged_decode: bad dtype");
   }
+}
+
+}  // namespace
+
+extern "C" int mlr_paged_decode(
+    const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *k_cache,
+    const void *v_cache, int64_t num_blocks, int64_t block_size,
+    int64_t num_kv_heads, int64_t head_dim, const int64_t *block_tables,
+    int64_t block_table_stride, int64_t max_blocks_per_seq,
+    const int64_t *context_lens, int64_t batch, int64_t num_q_heads,
+    double scale, int dtype, int64_t tokens_per_split, void *workspace,
+    size_t workspace_bytes, void *out, int64_t out_stride_b,
+    int64_t out_stride_h, void *stream) {
+  clear_error();
+  return run_decode(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                    block_size, num_kv_heads, head_dim, block_tables,
+                    block_table_stride, max_blocks_per_seq, context_lens, batch,
+                    num_q_heads, scale, dtype, tokens_per_split, workspace,
+                    workspace_bytes, out, out_stride_b, out_stride_h, stream,
+                    nullptr);
+}
+
+extern "C" int mlr_paged_decode_append(
+    const void *q, int64_t q_stride_b, int64_t q_stride_h, void *k_cache,
+    void *v_cache, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+    int64_t head_dim, const int64_t *block_tables, int64_t block_table_stride,
+    int64_t max_blocks_per_seq, const int64_t *context_lens, int64_t batch,
+    int64_t num_q_heads, double scale, int dtype, int64_t tokens_per_split,
+    void *workspace, size_t workspace_bytes, const void *new_k,
+    const void *new_v, int64_t new_stride_b, int64_t new_stride_h,
+    const int64_t *slot_mapping, void *out, int64_t out_stride_b,
+    int64_t out_stride_h, void *stream) {
+  clear_error();
+  const AppendArgs app{new_k, new_v, new_stride_b, new_stride_h, slot_mapping};
+  return run_decode(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                    block_size, num_kv_heads, head_dim, block_tables,
+                    block_table_stride, max_blocks_per_seq, context_lens, batch,
+                    num_q_heads, scale, dtype, tokens_per_split, workspace,
+                    workspace_bytes, out, out_stride_b, out_stride_h, stream,
+                    &app);
 }

@@ -187,7 +187,7 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
   }
 }
 
-template <int D, int kBatch, bool kDouble>
+template <int D, int kBatch, bool kDouble, bool kAppend>
 __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   constexpr int QK = D / 32;
   constexpr int VC = D / 16;
@@ -224,6 +224,23 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
     return idx < p.max_blocks ? bt_row[idx] : int64_t(-1);
   };
   int64_t blk_raw = raw_block_id(lane);
+  // Fused KV write: this lane's fragments of the new token's K and V rows and
+  // its slot, loaded with the rest of the prologue (used by at most one wave).
+  using VTa = typename VRow<D>::type;
+  uint4 new_kf[QK];
+  VTa new_vf{};
+  int64_t new_slot = -1;
+  if constexpr (kAppend) {
+    const uint16_t *nk_row = static_cast<const uint16_t *>(p.new_k) + b * p.new_sb +
+                             (int64_t)kvh * p.new_sh;
+    const uint16_t *nv_row = static_cast<const uint16_t *>(p.new_v) + b * p.new_sb +
+                             (int64_t)kvh * p.new_sh;
+#pragma unroll
+    for (int j = 0; j < QK; ++j)
+      new_kf[j] = *reinterpret_cast<const uint4 *>(nk_row + 32 * j + 8 * g);
+    new_vf = *reinterpret_cast<const VTa *>(nv_row + VC * m16);
+    new_slot = p.new_slots[b];
+  }
 
   const int64_t cap = p.max_blocks * p.block_size;
   const int64_t ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
@@ -266,6 +283,38 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   lo.v = ((4 * g * p.hkv + kvh) * D + VC * m16) * 2;
   lo.v_step = row_elems * 2;
   const int live = static_cast<int>(t1 - t0);
+  // Fused KV write: the new token (position ctx - 1) lives in the last tile of
+  // the last split. The wave that owns that tile stores the new K/V rows to
+  // slot new_slots[b] and, when that slot is the one position ctx - 1 maps to,
+  // uses the new rows in place of what it just read from the cache.
+  const int64_t last_pos = ctx - 1;
+  const bool append_here = kAppend && last_pos >= t0 && last_pos < t1;
+  const int last_rel = static_cast<int>(last_pos - t0) & ~15;  // tile of ctx - 1
+  const int last_tok = static_cast<int>(last_pos - t0) & 15;   // its row
+  auto append_token = [&](Tile<D> &t, int blk) {
+    const int64_t num_slots = p.num_blocks * p.block_size;
+    const bool slot_ok = new_slot >= 0 && new_slot < num_slots;
+    const bool same_slot =
+        blk >= 0 && new_slot == (int64_t)blk * p.block_size + last_pos % p.block_size;
+    uint16_t *kd = static_cast<uint16_t *>(p.kc_w) + (new_slot * p.hkv + kvh) * D;
+    uint16_t *vd = static_cast<uint16_t *>(p.vc_w) + (new_slot * p.hkv + kvh) * D;
+    if (m16 == last_tok) {  // lanes holding K row last_tok
+#pragma unroll
+      for (int j = 0; j < QK; ++j) {
+        if (slot_ok) *reinterpret_cast<uint4 *>(kd + 32 * j + 8 * g) = new_kf[j];
+        if (same_slot) t.k[j] = new_kf[j];
+      }
+    }
+    if (g == (last_tok >> 2)) {  // lanes holding V row last_tok (register last_tok & 3)
+      if (slot_ok) *reinterpret_cast<VTa *>(vd + VC * m16) = new_vf;
+      if (same_slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i == (last_tok & 3)) t.v[i] = new_vf;
+      }
+    }
+  };
+
   auto issue = [&](Tile<D>(&buf)[kBatch], int kb) {
     if ((kb & 63) == 0) load_block_ids(kb);
 #pragma unroll
@@ -276,6 +325,7 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
       // Byte offset of the tile's first token inside its block.
       const int tile_off = static_cast<int>((t0 + rel) % p.block_size) * row_elems * 2;
       load_tile<D>(buf[u], kc, vc, block_elems, tile_off, blk, rel, lo);
+      if (append_here && k < nk && rel == last_rel) append_token(buf[u], blk);
     }
   };
   auto compute = [&](Tile<D>(&buf)[kBatch]) {
@@ -415,17 +465,23 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
   // Tiles per wave: ceil(ts / 16 / 4). A split whose tiles fit one load batch
   // needs no second register buffer (fewer VGPRs, more waves per SIMD).
   const int tiles_per_wave = static_cast<int>(ceil_div(ceil_div(p.ts, 16), kWaves));
+  const bool append = p.new_k != nullptr;
+  // Instantiations: head_dim x (one load batch | double-buffered) x append.
+#define MLR_SPLIT(D_, B_, DB_)                                            \
+  (append ? (decode_split_mfma<D_, B_, DB_, true><<<grid, 256, 0, stream>>>(p)) \
+          : (decode_split_mfma<D_, B_, DB_, false><<<grid, 256, 0, stream>>>(p)))
   if (p.d == 64) {
     if (tiles_per_wave <= 4)
-      decode_split_mfma<64, 4, false><<<grid, 256, 0, stream>>>(p);
+      MLR_SPLIT(64, 4, false);
     else
-      decode_split_mfma<64, 4, true><<<grid, 256, 0, stream>>>(p);
+      MLR_SPLIT(64, 4, true);
   } else {
     if (tiles_per_wave <= 2)
-      decode_split_mfma<128, 2, false><<<grid, 256, 0, stream>>>(p);
+      MLR_SPLIT(128, 2, false);
     else
-      decode_split_mfma<128, 2, true><<<grid, 256, 0, stream>>>(p);
+      MLR_SPLIT(128, 2, true);
   }
+#undef MLR_SPLIT
   int rc = check_launch("mlr_paged_decode(split, mfma)");
   if (rc != MLR_OK) return rc;
   if (p.max_splits <= 1) return MLR_OK;  // every sequence fits one split

@@ -16,7 +16,10 @@ import threading
 import torch
 
 LIB_NAME = "libmlr_attn.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# MLR_ATTN_LIB names another build of the same library (e.g. to compare two
+# builds on one machine); by default the in-tree build next to this file.
+LIB_PATH = os.environ.get(
+    "MLR_ATTN_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
 
 # enum mlr_dtype / mlr_index_dtype in include/mlr_attn.h
 DTYPE_CODES = {
@@ -50,6 +53,13 @@ _PROTOTYPES = {
         [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_f64,
          _c_int, _c_i64, _c_ptr, _c_size, _c_ptr, _c_i64, _c_i64, _c_ptr],
+    ),
+    "mlr_paged_decode_append": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_f64,
+         _c_int, _c_i64, _c_ptr, _c_size, _c_ptr, _c_ptr, _c_i64, _c_i64,
+         _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr],
     ),
     "mlr_paged_prefill": (
         _c_int,

@@ -66,11 +66,17 @@ def paged_decode_launch(q: torch.Tensor, k_cache: torch.Tensor,
                         v_cache: torch.Tensor, block_tables: torch.Tensor,
                         seq_lens: torch.Tensor, out: torch.Tensor | None = None,
                         *, scale: float | None = None, tokens_per_split: int = 0,
-                        workspace: torch.Tensor | None = None) -> torch.Tensor:
+                        workspace: torch.Tensor | None = None,
+                        new_k: torch.Tensor | None = None,
+                        new_v: torch.Tensor | None = None,
+                        slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
     """Launch the split-KV decode on already-validated device operands.
 
     q [B, Hq, D]; k_cache/v_cache one contiguous layer [NB, BS, Hkv, D];
     block_tables [B, W] int64; seq_lens [B] int64, each in [1, W * BS].
+    With new_k/new_v [B, Hkv, D] (cache dtype) and slot_mapping [B] int64, the
+    decode step's KV write happens in the same call (mlr_paged_decode_append):
+    slot_mapping[b] must be the slot of position seq_lens[b] - 1.
     """
     device = _lib.require_hip(q, k_cache, v_cache, block_tables, seq_lens,
                               what="paged decode")
@@ -97,17 +103,28 @@ def paged_decode_launch(q: torch.Tensor, k_cache: torch.Tensor,
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
     stream = _lib.stream_handle(device)
+    common = (q.data_ptr(), q.stride(0), q.stride(1),
+              k_cache.data_ptr(), v_cache.data_ptr(),
+              num_blocks, block_size, num_kv_heads, head_dim,
+              block_tables.data_ptr(), block_tables.stride(0), width,
+              seq_lens.data_ptr(), batch, num_q_heads, float(scale), dcode,
+              int(tokens_per_split), workspace.data_ptr(), workspace.numel())
+    tail = (out.data_ptr(), out.stride(0), out.stride(1), stream)
+    if new_k is None:
+        with torch.cuda.device(device):
+            status = lib.mlr_paged_decode(*common, *tail)
+        _lib.check(status, "mlr_paged_decode")
+        return out
+    if new_k.dtype != k_cache.dtype or new_v.dtype != k_cache.dtype:
+        new_k, new_v = new_k.to(k_cache.dtype), new_v.to(k_cache.dtype)
+    if new_k.stride(-1) != 1 or new_k.stride() != new_v.stride():
+        new_k, new_v = new_k.contiguous(), new_v.contiguous()
+    slot_mapping = slot_mapping.to(torch.long).contiguous()
     with torch.cuda.device(device):
-        status = lib.mlr_paged_decode(
-            q.data_ptr(), q.stride(0), q.stride(1),
-            k_cache.data_ptr(), v_cache.data_ptr(),
-            num_blocks, block_size, num_kv_heads, head_dim,
-            block_tables.data_ptr(), block_tables.stride(0), width,
-            seq_lens.data_ptr(), batch, num_q_heads, float(scale), dcode,
-            int(tokens_per_split), workspace.data_ptr(), workspace.numel(),
-            out.data_ptr(), out.stride(0), out.stride(1),
-            stream)
-    _lib.check(status, "mlr_paged_decode")
+        status = lib.mlr_paged_decode_append(
+            *common, new_k.data_ptr(), new_v.data_ptr(), new_k.stride(0),
+            new_k.stride(1), slot_mapping.data_ptr(), *tail)
+    _lib.check(status, "mlr_paged_decode_append")
     return out
 
 

@@ -115,6 +115,36 @@ def test_split_size_does_not_change_the_result(device, tokens_per_split):
     assert max_abs(got, want) <= 2e-2
 
 
+@pytest.mark.parametrize("dtype,lens,tokens_per_split", [
+    (torch.bfloat16, [1, 16, 17, 300, 1000, 257], 0),     # fused in the MFMA kernel
+    (torch.bfloat16, [33, 64, 500], 64),
+    (torch.float32, [5, 255, 256], 0),                     # write kernel, then decode
+])
+def test_decode_append_equals_write_then_decode(device, dtype, lens, tokens_per_split):
+    """mlr_paged_decode_append: same cache bits and same output bits as
+    write_slots followed by paged decode."""
+    q, kc, vc, bt, sl, tables = random_paged(lens, 14, 2, 64, 16, dtype=dtype, seed=21,
+                                             fill=0.0)
+    gen = torch.Generator().manual_seed(5)
+    new_k = torch.randn(len(lens), 2, 64, generator=gen).to(dtype)
+    new_v = torch.randn(len(lens), 2, 64, generator=gen).to(dtype)
+    slots = torch.tensor([tables[b][(n - 1) // 16] * 16 + (n - 1) % 16
+                          for b, n in enumerate(lens)])
+    q, bt, sl, slots_d = (t.to(device) for t in (q, bt, sl, slots))
+    k1, v1 = kc.to(device), vc.to(device)
+    k2, v2 = kc.to(device), vc.to(device)
+    nk, nv = new_k.to(device), new_v.to(device)
+    fused = kpa.paged_decode_launch(q, k1, v1, bt, sl, new_k=nk, new_v=nv,
+                                    slot_mapping=slots_d, tokens_per_split=tokens_per_split)
+    k2.view(-1, 2, 64).index_copy_(0, slots_d, nk)
+    v2.view(-1, 2, 64).index_copy_(0, slots_d, nv)
+    plain = kpa.paged_decode_launch(q, k2, v2, bt, sl, tokens_per_split=tokens_per_split)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(fused, plain)
+    want = opa.decode_batch_loop(q.cpu(), k2.cpu(), v2.cpu(), tables, lens, 16)
+    assert max_abs(fused, want) <= TOL[dtype]
+
+
 def test_batch_permutation_is_bitwise_invariant(device):
     q, kc, vc, bt, sl, _ = random_paged([64, 129, 1024, 3000, 17], 14, 2, 64, 16,
                                         dtype=torch.bfloat16, seed=9)
