@@ -146,6 +146,14 @@ __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) {
   return (a + b - 1) / b;
 }
 
+// log2(x) when x is a positive power of two, else -1.
+inline int log2_if_pow2(int64_t x) {
+  if (x <= 0 || (x & (x - 1)) != 0) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < x) ++s;
+  return s;
+}
+
 inline int dtype_size(int dtype) {
   switch (dtype) {
     case MLR_DTYPE_F32: return 4;

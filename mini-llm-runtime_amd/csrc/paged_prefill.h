@@ -26,6 +26,7 @@ struct PrefillParams {
   int group;
   double scale;
   int kv_tile;
+  int bs_log2;  // log2(block_size) when it is a power of two, else -1
   void *out;
   int64_t o_st, o_sh;
 };

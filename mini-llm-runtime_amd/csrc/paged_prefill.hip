@@ -152,16 +152,18 @@ int launch_generic(const PrefillParams &p, int64_t max_qlen,
   return check_launch("mlr_paged_prefill");
 }
 
-int run_prefill(const PrefillParams &p, int dtype, int64_t max_qlen,
+int run_prefill(const PrefillParams &params, int dtype, int64_t max_qlen,
                 hipStream_t stream) {
   if (max_qlen <= 0) return MLR_OK;
+  PrefillParams p = params;
+  p.bs_log2 = log2_if_pow2(p.block_size);
   const bool aligned = (reinterpret_cast<uintptr_t>(p.q) & 15u) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.kc) & 15u) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.vc) & 15u) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0 &&
                        p.q_st % 8 == 0 && p.q_sh % 8 == 0 && p.o_st % 8 == 0 &&
                        p.o_sh % 8 == 0;
-  if (aligned && prefill_mfma_eligible(dtype, p.d, p.block_size))
+  if (aligned && p.bs_log2 >= 0 && prefill_mfma_eligible(dtype, p.d, p.block_size))
     return launch_prefill_mfma(p, max_qlen, stream);
   switch (dtype) {
     case MLR_DTYPE_F32: return launch_generic<float>(p, max_qlen, stream);

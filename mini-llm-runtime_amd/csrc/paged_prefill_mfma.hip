@@ -19,8 +19,8 @@
 //   O^T[D x 16 queries] += V^T[D x 32 keys] . P^T[32 keys x 16 queries]
 //       B = P^T straight from the S^T registers of two 16-key blocks (k slot
 //       8g+i <-> key 16*(2kp + i/4) + 4g + i%4), rounded to bf16; A = V^T,
-//       which the loader stores transposed ([dim][key]) so a lane's eight
-//       keys are two 8-byte LDS reads.
+//       read from the row-major V tile with ds_read_b64_tr_b16 (two per
+//       MFMA), which transposes 16-bit elements across 16 lanes.
 // Causal masking (key position <= query position, both absolute) is applied
 // only on tiles that reach the workgroup's first query position; keys past
 // the last position any of its queries can see are neither loaded nor used.
@@ -38,6 +38,9 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) unsigned char lds_t;    // LDS bytes
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;
@@ -46,9 +49,9 @@ constexpr int kBM = 64;  // queries per workgroup
 template <int D, int BN>
 struct PrefillCfg {
   static constexpr int kKRow = D * 2 + 16;    // bytes per K row in LDS
-  static constexpr int kVRow = BN * 2 + 16;   // bytes per V^T row in LDS
+  static constexpr int kVRow = D * 2 + 16;    // bytes per V row in LDS
   static constexpr int kKBytes = BN * kKRow;
-  static constexpr int kVBytes = D * kVRow;
+  static constexpr int kVBytes = BN * kVRow;
   static constexpr int kStage = kKBytes + kVBytes;
   static constexpr int kTpk = 256 / BN;          // loader threads per key
   static constexpr int kDpt = D / kTpk;          // dims per loader thread
@@ -56,15 +59,17 @@ struct PrefillCfg {
   static_assert(kChunks >= 1, "tile too large for this head_dim");
 };
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to packed bf16 (round to nearest even): one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
-  const __bf16 a = static_cast<__bf16>(lo);
-  const __bf16 b = static_cast<__bf16>(hi);
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+  const bf16x2_t v = __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <int D, int BN>
-__global__ __launch_bounds__(256) void prefill_mfma(PrefillParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void prefill_mfma(PrefillParams p) {
   using C = PrefillCfg<D, BN>;
   constexpr int QS = D / 32;   // k-steps of S^T
   constexpr int NB = D / 16;   // 16-dim blocks of O^T
@@ -94,6 +99,7 @@ __global__ __launch_bounds__(256) void prefill_mfma(PrefillParams p) {
   const int64_t qi = q0 + 16 * w + m16;
   const bool q_ok = qi < r.qlen;
   const int64_t qpos = r.prefix + qi;
+  const int qpos32 = static_cast<int>(qpos);
   const uint16_t *qrow = static_cast<const uint16_t *>(p.q) +
                          (r.q0 + (q_ok ? qi : 0)) * p.q_st + (int64_t)h * p.q_sh;
   bf16x8_t qf[QS];
@@ -110,16 +116,21 @@ __global__ __launch_bounds__(256) void prefill_mfma(PrefillParams p) {
   const uint16_t *kc = static_cast<const uint16_t *>(p.kc);
   const uint16_t *vc = static_cast<const uint16_t *>(p.vc);
   const int64_t *bt_row = p.bt + seq * p.bt_stride;
+  // Positions fit 32 bits; block_size is a power of two on this path.
+  const int bs_log2 = p.bs_log2;
+  const int bs_mask = (1 << bs_log2) - 1;
+  const int kv_end32 = static_cast<int>(kv_end);
   auto block_of = [&](int t) -> int64_t {
-    const int64_t pos = static_cast<int64_t>(t) * BN + kk;
-    if (pos >= kv_end) return -1;
-    const int64_t blk = bt_row[pos / p.block_size];
+    const int pos = t * BN + kk;
+    if (pos >= kv_end32) return -1;
+    const int64_t blk = bt_row[pos >> bs_log2];
     return (blk >= 0 && blk < p.num_blocks) ? blk : -1;
   };
   uint4 kreg[C::kChunks], vreg[C::kChunks];
   auto load_rows = [&](int t, int64_t blk) {
-    const int64_t pos = static_cast<int64_t>(t) * BN + kk;
-    const int64_t off = ((blk * p.block_size + pos % p.block_size) * p.hkv + kvh) * D + dc;
+    const int pos = t * BN + kk;
+    const int64_t off =
+        (((blk << bs_log2) + (pos & bs_mask)) * p.hkv + kvh) * int64_t(D) + dc;
 #pragma unroll
     for (int c = 0; c < C::kChunks; ++c) {
       // Absent keys load zeros: masked keys must not carry NaN into P@V.
@@ -132,16 +143,10 @@ __global__ __launch_bounds__(256) void prefill_mfma(PrefillParams p) {
   auto store_rows = [&](int stage) {
     unsigned char *base = smem + stage * C::kStage;
 #pragma unroll
-    for (int c = 0; c < C::kChunks; ++c)
-      *reinterpret_cast<uint4 *>(base + kk * C::kKRow + (dc + 8 * c) * 2) = kreg[c];
-    uint16_t *vt = reinterpret_cast<uint16_t *>(base + C::kKBytes);
-#pragma unroll
     for (int c = 0; c < C::kChunks; ++c) {
-      const uint32_t wv[4] = {vreg[c].x, vreg[c].y, vreg[c].z, vreg[c].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        vt[(dc + 8 * c + e) * (C::kVRow / 2) + kk] =
-            static_cast<uint16_t>(e & 1 ? wv[e >> 1] >> 16 : wv[e >> 1] & 0xffffu);
+      *reinterpret_cast<uint4 *>(base + kk * C::kKRow + (dc + 8 * c) * 2) = kreg[c];
+      *reinterpret_cast<uint4 *>(base + C::kKBytes + kk * C::kVRow + (dc + 8 * c) * 2) =
+          vreg[c];
     }
   };
 
@@ -153,7 +158,7 @@ __global__ __launch_bounds__(256) void prefill_mfma(PrefillParams p) {
 
   auto compute = [&](int t, int stage) {
     const unsigned char *base = smem + stage * C::kStage;
-    const int64_t tile0 = static_cast<int64_t>(t) * BN;
+    const int tile0 = t * BN;
     f32x4_t s[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -170,7 +175,7 @@ __global__ __launch_bounds__(256) void prefill_mfma(PrefillParams p) {
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (tile0 + 16 * kb + 4 * g + i > qpos) s[kb][i] = -INFINITY;
+          if (tile0 + 16 * kb + 4 * g + i > qpos32) s[kb][i] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -207,14 +212,21 @@ __global__ __launch_bounds__(256) void prefill_mfma(PrefillParams p) {
                      bf16_pack2(pr[2 * kp][2], pr[2 * kp][3]),
                      bf16_pack2(pr[2 * kp + 1][0], pr[2 * kp + 1][1]),
                      bf16_pack2(pr[2 * kp + 1][2], pr[2 * kp + 1][3])));
-      const uint16_t *vt = reinterpret_cast<const uint16_t *>(base + C::kKBytes);
+      // A = V^T from the row-major V tile with ds_read_b64_tr_b16: in each
+      // 16-lane group, lane r points at V[kbase + r/4][dim0 + 4(r%4) .. +4)
+      // and lane i receives V[kbase + 0..3][dim0 + i] (kbase = 32kp + 4g,
+      // then +16 for slots 4..7; dim0 = 16n).
+      lds_t *vrow0 = (lds_t *)(base + C::kKBytes +
+                               (32 * kp + 4 * g + (m16 >> 2)) * C::kVRow + (m16 & 3) * 8);
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        const uint16_t *row = vt + (16 * n + m16) * (C::kVRow / 2) + 32 * kp + 4 * g;
-        const uint2 lo = *reinterpret_cast<const uint2 *>(row);
-        const uint2 hi = *reinterpret_cast<const uint2 *>(row + 16);
-        const bf16x8_t a =
-            __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        const s16x4_t lo =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vrow0 + 32 * n));
+        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4_t *)(vrow0 + 32 * n + 16 * C::kVRow));
+        const bf16x8_t a = __builtin_bit_cast(
+            bf16x8_t, make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                 __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y));
         acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, acc[n], 0, 0, 0);
       }
     }
