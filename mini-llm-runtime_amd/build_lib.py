@@ -27,6 +27,9 @@ HIPCC_FLAGS = [
     "-shared",
     # Packed FP32 VALU ops stay off: scalar FP32 code only.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the softmax reads them every tile,
+    # and the AGPR form would add a v_accvgpr_read per value.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -27,6 +27,7 @@ struct PrefillParams {
   double scale;
   int kv_tile;
   int bs_log2;  // log2(block_size) when it is a power of two, else -1
+  int n_qtiles; // query tiles per sequence (matrix-core kernel only)
   void *out;
   int64_t o_st, o_sh;
 };
@@ -58,7 +59,9 @@ __device__ __forceinline__ SeqRange seq_range(const PrefillParams &p, int s) {
   return r;
 }
 
-bool prefill_mfma_eligible(int dtype, int64_t head_dim, int64_t block_size);
+// True when the bf16 matrix-core kernel covers these arguments (bf16, head_dim
+// 64 or 128, power-of-two block_size >= 16, aligned rows, positive scale).
+bool prefill_mfma_eligible(const PrefillParams &p, int dtype);
 int launch_prefill_mfma(const PrefillParams &p, int64_t max_query_len,
                         hipStream_t stream);
 

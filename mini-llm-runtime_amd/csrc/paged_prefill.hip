@@ -157,13 +157,7 @@ int run_prefill(const PrefillParams &params, int dtype, int64_t max_qlen,
   if (max_qlen <= 0) return MLR_OK;
   PrefillParams p = params;
   p.bs_log2 = log2_if_pow2(p.block_size);
-  const bool aligned = (reinterpret_cast<uintptr_t>(p.q) & 15u) == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.kc) & 15u) == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.vc) & 15u) == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0 &&
-                       p.q_st % 8 == 0 && p.q_sh % 8 == 0 && p.o_st % 8 == 0 &&
-                       p.o_sh % 8 == 0;
-  if (aligned && p.bs_log2 >= 0 && prefill_mfma_eligible(dtype, p.d, p.block_size))
+  if (prefill_mfma_eligible(p, dtype))
     return launch_prefill_mfma(p, max_qlen, stream);
   switch (dtype) {
     case MLR_DTYPE_F32: return launch_generic<float>(p, max_qlen, stream);

@@ -1,66 +1,84 @@
-// bf16 paged chunk prefill on gfx950 matrix cores.
+// bf16 paged chunk prefill on gfx950 matrix cores (v_mfma_f32_32x32x16_bf16).
 //
-// One workgroup = 64 queries of one query head (four waves x 16 queries).
-// Keys stream in tiles of kBN positions through two LDS stages: while a tile
-// is being used, the next tile's rows are already in flight from HBM into
-// registers, and the block ids of the tile after that are in flight too.
+// One workgroup = 128 queries of one query head, four waves of 32 queries.
+// Keys stream through LDS in tiles of BN positions (128 for head_dim 64, 64
+// for head_dim 128) and two stages: while the waves compute on one stage, the
+// next tile is copied from HBM straight into the other stage with
+// buffer_load_dwordx4 ... lds (no register staging). Each wave copies BN/4
+// consecutive key rows of K and of V, as spans of 16 rows. With block_size a
+// power of two >= 16 a span sits in one cache block, so its source address is
+// scalar (block id and slot base, in a buffer resource) plus a lane-constant
+// offset. Rows past the last key the workgroup needs, and the spans of
+// out-of-range blocks, fall outside the buffer resource and read as zeros;
+// keys of an out-of-range block are also masked.
 //
-// Per tile and wave (16 queries x kBN keys), with v_mfma_f32_16x16x32_bf16:
-//   S^T[16 keys x 16 queries] = K[16 keys x D] . Q^T[D x 16 queries]
-//       A = K rows from LDS (row-major, rows padded by 16 bytes so the 16 row
-//       reads of one instruction fall in distinct banks); B = Q^T fragments
-//       held in registers for the whole kernel.
-//   base-2 online softmax in FP32: lane l owns query l%16 and keys
-//       4(l/16)..+3 of each 16-key block; the row max is two cross-row
-//       shuffles. The running max moves only when a tile raises it by more
-//       than kLazy (base-2 units): until then the accumulators keep their
-//       scale and probabilities may reach 2^kLazy (exact either way, since
-//       numerator and denominator share the reference point).
-//   O^T[D x 16 queries] += V^T[D x 32 keys] . P^T[32 keys x 16 queries]
-//       B = P^T straight from the S^T registers of two 16-key blocks (k slot
-//       8g+i <-> key 16*(2kp + i/4) + 4g + i%4), rounded to bf16; A = V^T,
-//       read from the row-major V tile with ds_read_b64_tr_b16 (two per
-//       MFMA), which transposes 16-bit elements across 16 lanes.
-// Causal masking (key position <= query position, both absolute) is applied
-// only on tiles that reach the workgroup's first query position; keys past
-// the last position any of its queries can see are neither loaded nor used.
+// LDS rows are unpadded (2*D bytes). The 16-byte chunk c of tile row r is
+// stored at chunk c ^ swz(r), which keeps both the K reads of S^T and the
+// transposing V reads of P@V free of bank conflicts.
+//
+// Per tile and wave (32 queries x BN keys):
+//   S^T[32 keys x 32 queries] = K[32 keys x D] . Q^T[D x 32 queries] for each
+//       32-key block of the tile, D/16 MFMAs each; A = K rows (ds_read_b128),
+//       B = Q^T fragments held in registers throughout.
+//   Lane l owns query l%32 and keys 8(i/4) + 4(l/32) + i%4 (i < 16) of each
+//   32-key block; lanes l and l^32 share a query, so the row max is one
+//   permlane32 swap. Base-2 online softmax in FP32; the reference point moves
+//   only when a tile raises the row max by more than kLazy (base-2 units), so
+//   probabilities stay below 2^kLazy and numerator and denominator share it.
+//   O^T[32 dims x 32 queries] += V^T[32 dims x 16 keys] . P^T[16 keys x 32 q]
+//       B = P^T packed to bf16 straight from the S^T registers (k slot
+//       8(l/32)+e <-> key 16kb + 8(e/4) + 4(l/32) + e%4), A = V^T from two
+//       ds_read_b64_tr_b16 per MFMA.
+//   The row sums add the FP32 probabilities, as the reference does.
+// Causal masking (key position <= query position, both absolute) runs only
+// on tiles that reach the wave's first query position; a wave skips the
+// tiles past its last query position.
 //
 // Numerics follow paged_attention_prefill_chunk_tiled
-// (kernels/reference/paged_attention.py:346-434): FP32 softmax statistics
-// and FP32 accumulation of P@V, one rounding of the output. P is rounded to
-// bf16 as the MFMA operand, and the scores are not rounded to bf16 first
-// (the reference rounds q.k to bf16 at :411-413); both stay far inside the
-// 2e-2 tolerance the reference's own bf16 tests use.
+// (kernels/reference/paged_attention.py:346-434): FP32 softmax statistics,
+// FP32 accumulation of P@V and one rounding of the output. Two roundings
+// differ from the reference and stay far inside the 2e-2 tolerance of its
+// bf16 tests: P is rounded to bf16 as the MFMA operand, and q.k is not
+// rounded to bf16 before scaling (the reference rounds at :411-413).
 #include "paged_prefill.h"
 
 namespace mlr {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) unsigned char lds_t;    // LDS bytes
+typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;
-constexpr int kBM = 64;  // queries per workgroup
+constexpr float kFloor = -1.0e30f;  // initial reference point (base 2)
+constexpr int kBM = 128;      // queries per workgroup (4 waves x 32)
+constexpr int kSpanRows = 16; // key rows per copy span
+constexpr int kRankMax = 512; // most work items ranked in the prologue
+constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads zeros
 
 template <int D, int BN>
-struct PrefillCfg {
-  static constexpr int kKRow = D * 2 + 16;    // bytes per K row in LDS
-  static constexpr int kVRow = D * 2 + 16;    // bytes per V row in LDS
-  static constexpr int kKBytes = BN * kKRow;
-  static constexpr int kVBytes = BN * kVRow;
-  static constexpr int kStage = kKBytes + kVBytes;
-  static constexpr int kTpk = 256 / BN;          // loader threads per key
-  static constexpr int kDpt = D / kTpk;          // dims per loader thread
-  static constexpr int kChunks = kDpt / 8;       // 16-byte chunks per thread
-  static_assert(kChunks >= 1, "tile too large for this head_dim");
+struct Cfg {
+  static constexpr int kRowB = 2 * D;                        // LDS bytes per key row
+  static constexpr int kTileB = BN * kRowB;                  // one K (or V) tile
+  static constexpr int kChunks = D / 8;                      // 16-byte chunks per row
+  static constexpr int kSpans = BN / 4 / kSpanRows;          // spans per wave and tile
+  static constexpr int kCopies = kSpanRows * kRowB / 1024;   // 1 KB copies per span
+  static constexpr int kBlocks = BN / 32;                    // 32-key blocks per tile
+  static_assert(kSpans >= 1 && kSpans <= 2, "tile must hold 4 or 8 spans");
 };
 
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// Chunk swizzle (depends on the low four row bits only, so it repeats every
+// 16 rows): physical chunk = logical chunk ^ swz(row).
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if (D == 64) return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+  return ((r & 1) << 1) | (((r >> 1) & 3) << 2) | ((r >> 3) & 1);
+}
 
 // Two floats to packed bf16 (round to nearest even): one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
@@ -68,227 +86,440 @@ __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int D, int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void prefill_mfma(PrefillParams p) {
-  using C = PrefillCfg<D, BN>;
-  constexpr int QS = D / 32;   // k-steps of S^T
-  constexpr int NB = D / 16;   // 16-dim blocks of O^T
-  constexpr int KB = BN / 16;  // 16-key blocks per tile
-  constexpr int KP = BN / 32;  // 32-key steps of P@V
-  extern __shared__ __align__(16) unsigned char smem[];
+// max(a, b, c) as one v_maximum3_f32 (NaN-propagating, no canonicalisation).
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
 
-  // Grid (query head, sequence, query tile), query tiles last-first: the
-  // tiles with the most keys start first.
-  const int h = blockIdx.x, seq = blockIdx.y;
-  const int qt = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
+// Lanes l and l ^ 32 exchange x (one v_permlane32_swap): the two halves of
+// the result hold x of the lower and of the upper half-wave.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// KS splits of the workgroup's key range run side by side: waves 4k..4k+3
+// take the k-th contiguous share of the tiles for the same 128 queries, and
+// the splits are merged through LDS at the end. A long sequence's critical path
+// shrinks by KS.
+template <int D, int BN, int KS>
+__global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2)))
+void prefill_mfma(PrefillParams p) {
+  using C = Cfg<D, BN>;
+  constexpr int QS = D / 16;         // 16-dim k-steps of S^T
+  constexpr int NB = D / 32;         // 32-dim blocks of O^T
+  constexpr int KB = C::kBlocks;     // 32-key blocks per tile
+  constexpr int NSP = C::kSpans;
+  // Per split: two stages of K and of V, each a separate LDS object, so that
+  // reads of one stage need not wait for copies into another.
+  // badkS[k][span] is set when that 16-row span of split k's K tile in stage
+  // S lies in an out-of-range block.
+  __shared__ __align__(1024) unsigned char ks0[KS][C::kTileB];
+  __shared__ __align__(1024) unsigned char ks1[KS][C::kTileB];
+  __shared__ __align__(1024) unsigned char vs0[KS][C::kTileB];
+  __shared__ __align__(1024) unsigned char vs1[KS][C::kTileB];
+  __shared__ __align__(8) unsigned char badk0[KS][8];
+  __shared__ __align__(8) unsigned char badk1[KS][8];
+
+  // Work items are (sequence, query tile) pairs, each run once per query head.
+  // Workgroups start in order of blockIdx.x, and the hardware hands a freed
+  // CU the next one, so the items are taken longest first (list scheduling):
+  // blockIdx.x = rank * hq + head, where rank orders the items by the keys
+  // they need, longest first, ties by item index. With more than kRankMax
+  // items the ranking is skipped and items go sequence by sequence, last
+  // query tile first.
+  const int nqt = p.n_qtiles;
+  const int nitems = p.num_seqs * nqt;
+  const int rank = static_cast<int>(blockIdx.x) / p.hq;
+  const int h = static_cast<int>(blockIdx.x) % p.hq;
+  int item;
+  if (nitems <= kRankMax) {
+    __shared__ int item_len[kRankMax];
+    __shared__ int ranked_item;
+    auto keys_of = [&](int i) __attribute__((always_inline)) -> int {
+      const SeqRange r = seq_range(p, i / nqt);
+      const int64_t lo = static_cast<int64_t>(i % nqt) * kBM;
+      return lo < r.qlen ? static_cast<int>(r.prefix + min<int64_t>(r.qlen, lo + kBM)) : 0;
+    };
+    for (int i = threadIdx.x; i < nitems; i += blockDim.x) item_len[i] = keys_of(i);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nitems; i += blockDim.x) {
+      const int li = item_len[i];
+      int r = 0;
+      for (int j = 0; j < nitems; ++j) {
+        const int lj = item_len[j];
+        r += (lj > li || (lj == li && j < i)) ? 1 : 0;
+      }
+      if (r == rank) ranked_item = i;
+    }
+    __syncthreads();
+    item = ranked_item;
+  } else {
+    item = (rank / nqt) * nqt + (nqt - 1 - rank % nqt);
+  }
+  const int seq = item / nqt, qt = item % nqt;
+  const SeqRange rg = seq_range(p, seq);
+  const int q0 = qt * kBM;
+  if (q0 >= rg.qlen) return;  // uniform
   const int kvh = h / p.group;
-  const SeqRange r = seq_range(p, seq);
-  const int64_t q0 = static_cast<int64_t>(qt) * kBM;
-  if (q0 >= r.qlen) return;  // uniform
+  const int qlen = static_cast<int>(rg.qlen), prefix = static_cast<int>(rg.prefix);
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int m16 = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = wv & 3, split = wv >> 2;  // query group, key-range split
+  const int m32 = lane & 31, hh = lane >> 5;
 
-  const int64_t kv_end = r.prefix + min<int64_t>(r.qlen, q0 + kBM);  // keys used
-  const int ntiles = static_cast<int>(ceil_div(kv_end, BN));
-  // Tiles below nfull end before the first query position: no mask needed.
-  const int nfull = static_cast<int>((r.prefix + q0) / BN);
+  // Keys the workgroup needs: up to its last query position; split k takes
+  // tiles [t_lo, t_hi).
+  const int kv_end = prefix + min(qlen, q0 + kBM);
+  const int ntiles = (kv_end + BN - 1) / BN;
+  const int chunk = (ntiles + KS - 1) / KS;
+  const int t_lo = split * chunk, t_hi = min(ntiles, t_lo + chunk);
+  // This wave's queries [wq, wq_end); tiles it reads; tiles it sees whole.
+  const int wq = q0 + 32 * w;
+  const int wq_end = min(qlen, wq + 32);
+  const int wave_tiles = wq < wq_end ? min(t_hi, (prefix + wq_end - 1) / BN + 1) : 0;
+  const int wave_nfull = (prefix + wq + 1) / BN;
 
-  // Q^T fragments: lane l holds Q[query 16w + l%16][32s + 8g .. +8).
-  const int64_t qi = q0 + 16 * w + m16;
-  const bool q_ok = qi < r.qlen;
-  const int64_t qpos = r.prefix + qi;
-  const int qpos32 = static_cast<int>(qpos);
+  // Q^T fragments: lane l holds Q[query wq + l%32][16s + 8(l/32) .. +8).
+  const int qi = wq + m32;
+  const bool q_ok = qi < qlen;
+  const int qpos = prefix + qi;
   const uint16_t *qrow = static_cast<const uint16_t *>(p.q) +
-                         (r.q0 + (q_ok ? qi : 0)) * p.q_st + (int64_t)h * p.q_sh;
+                         (rg.q0 + (q_ok ? qi : 0)) * p.q_st + static_cast<int64_t>(h) * p.q_sh;
   bf16x8_t qf[QS];
 #pragma unroll
   for (int s = 0; s < QS; ++s) {
-    const uint4 raw = q_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * s + 8 * g)
+    const uint4 raw = q_ok ? *reinterpret_cast<const uint4 *>(qrow + 16 * s + 8 * hh)
                            : make_uint4(0, 0, 0, 0);
     qf[s] = __builtin_bit_cast(bf16x8_t, raw);
   }
 
-  // Loader role: key kk of a tile, dims [dc, dc + kDpt).
-  const int kk = tid / C::kTpk;
-  const int dc = (tid % C::kTpk) * C::kDpt;
-  const uint16_t *kc = static_cast<const uint16_t *>(p.kc);
-  const uint16_t *vc = static_cast<const uint16_t *>(p.vc);
-  const int64_t *bt_row = p.bt + seq * p.bt_stride;
-  // Positions fit 32 bits; block_size is a power of two on this path.
+  // Copy role: copy i of a span moves chunk positions [64i, 64i + 64) of its 16
+  // rows; lane l fills position 64i + l (row rr, physical chunk pc) with
+  // logical chunk pc ^ swz(rr) of source row rr.
+  const uint32_t row_bytes = static_cast<uint32_t>(p.hkv) * D * 2;  // slot stride
+  uint32_t src_off[C::kCopies];
+  int src_row[C::kCopies];
+#pragma unroll
+  for (int i = 0; i < C::kCopies; ++i) {
+    const int pos = 64 * i + lane;
+    const int rr = pos / C::kChunks, pc = pos % C::kChunks;
+    src_row[i] = rr;
+    src_off[i] = rr * row_bytes + ((pc ^ swz<D>(rr)) << 4);
+  }
+  const int64_t *bt_row = p.bt + static_cast<int64_t>(seq) * p.bt_stride;
   const int bs_log2 = p.bs_log2;
   const int bs_mask = (1 << bs_log2) - 1;
-  const int kv_end32 = static_cast<int>(kv_end);
-  auto block_of = [&](int t) -> int64_t {
-    const int pos = t * BN + kk;
-    if (pos >= kv_end32) return -1;
-    const int64_t blk = bt_row[pos >> bs_log2];
-    return (blk >= 0 && blk < p.num_blocks) ? blk : -1;
+  // First position of span sp of this wave in tile t.
+  auto span_pos = [&](int t, int sp) __attribute__((always_inline)) -> int {
+    return t * BN + (BN / 4) * w + kSpanRows * sp;
   };
-  uint4 kreg[C::kChunks], vreg[C::kChunks];
-  auto load_rows = [&](int t, int64_t blk) {
-    const int pos = t * BN + kk;
-    const int64_t off =
-        (((blk << bs_log2) + (pos & bs_mask)) * p.hkv + kvh) * int64_t(D) + dc;
+  // Block ids of the wave's spans in tile t (the same in every lane); the
+  // lookup is clamped into the table.
+  auto block_ids = [&](int t, int64_t (&ids)[NSP]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < C::kChunks; ++c) {
-      // Absent keys load zeros: masked keys must not carry NaN into P@V.
-      kreg[c] = blk >= 0 ? *reinterpret_cast<const uint4 *>(kc + off + 8 * c)
-                         : make_uint4(0, 0, 0, 0);
-      vreg[c] = blk >= 0 ? *reinterpret_cast<const uint4 *>(vc + off + 8 * c)
-                         : make_uint4(0, 0, 0, 0);
+    for (int sp = 0; sp < NSP; ++sp)
+      ids[sp] = bt_row[min(span_pos(t, sp), kv_end - 1) >> bs_log2];
+  };
+  // Copies the wave's spans of tile t from `cache` into the LDS tile `dst`;
+  // with `bad`, also records which spans lie in out-of-range blocks.
+  auto issue = [&](int t, const int64_t (&ids)[NSP], const void *cache, unsigned char *dst,
+                   unsigned char *bad) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sp = 0; sp < NSP; ++sp) {
+      const int pos0 = span_pos(t, sp);
+      const int64_t blk = uniform64(ids[sp]);
+      const bool live = pos0 < kv_end;
+      const bool ok = live && blk >= 0 && blk < p.num_blocks;
+      const int64_t slot = ok ? (blk << bs_log2) + (pos0 & bs_mask) : 0;
+      const int64_t byte0 = (slot * p.hkv + kvh) * (2 * D);
+      const uint32_t nrec = ok ? 15u * row_bytes + 2u * D : 0u;
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<unsigned char *>(static_cast<const unsigned char *>(cache) + byte0), 0,
+          nrec, 0x00020000);
+      const int nrows = kv_end - pos0;  // rows of the span that are needed
+      unsigned char *sdst = dst + ((BN / 4) * w + kSpanRows * sp) * C::kRowB;
+#pragma unroll
+      for (int i = 0; i < C::kCopies; ++i) {
+        const uint32_t off = src_row[i] < nrows ? src_off[i] : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(sdst + 1024 * i), 16, off,
+                                                 0, 0, 0);
+      }
+      if (bad != nullptr && lane == 0) bad[NSP * w + sp] = (live && !ok) ? 1 : 0;
     }
   };
-  auto store_rows = [&](int stage) {
-    unsigned char *base = smem + stage * C::kStage;
-#pragma unroll
-    for (int c = 0; c < C::kChunks; ++c) {
-      *reinterpret_cast<uint4 *>(base + kk * C::kKRow + (dc + 8 * c) * 2) = kreg[c];
-      *reinterpret_cast<uint4 *>(base + C::kKBytes + kk * C::kVRow + (dc + 8 * c) * 2) =
-          vreg[c];
+  auto read_bad = [&](const unsigned char *bad) __attribute__((always_inline)) -> uint64_t {
+    if constexpr (NSP == 2) {
+      const uint2 b = *reinterpret_cast<const uint2 *>(bad);
+      return (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(b.y)) << 32) |
+             __builtin_amdgcn_readfirstlane(b.x);
+    } else {
+      return __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(bad));
     }
   };
 
-  const float c2 = static_cast<float>(p.scale) * kLog2e;  // score -> base-2
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4_t acc[NB];
+  // Lane-constant LDS offsets. K read of step st: row m32 (+32 per key block),
+  // logical chunk 2st + hh. V^T read (two per MFMA, rows +8 apart): in each
+  // 16-lane group G, lane li points at row 4(G/2) + li/4 (+ 16kb) and byte
+  // 64n + 32(G%2) + 8(li%4).
+  int koff[QS];
 #pragma unroll
-  for (int n = 0; n < NB; ++n) acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int st = 0; st < QS; ++st)
+    koff[st] = m32 * C::kRowB + (((2 * st + hh) ^ swz<D>(m32)) << 4);
+  const int G = lane >> 4, li = lane & 15;
+  int voff[2][NB];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      const int row = 4 * (G >> 1) + (li >> 2) + 8 * half;
+      const int byte = 64 * n + 32 * (G & 1) + 8 * (li & 3);
+      voff[half][n] = row * C::kRowB + ((((byte >> 4) ^ swz<D>(row)) << 4) | (byte & 15));
+    }
 
-  auto compute = [&](int t, int stage) {
-    const unsigned char *base = smem + stage * C::kStage;
-    const int tile0 = t * BN;
-    f32x4_t s[KB];
+  const float c2 = static_cast<float>(p.scale) * kLog2e;  // score -> base 2
+  // Reference point of the running softmax (base 2). It starts at a finite
+  // floor, not -inf: a query can see no key at all in one split's tiles, and
+  // exp2(-inf - (-inf)) would be NaN. Masked scores stay -inf, so their
+  // probabilities are exactly 0 under any reference point.
+  float m_run = kFloor, l_run = 0.f;
+  f32x16_t acc[NB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      s[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n < NB; ++n)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[n][i] = 0.f;
+
+  // S^T of one tile from its K stage.
+  auto scores = [&](const unsigned char *kst, f32x16_t (&s)[KB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[j][i] = 0.f;
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
-        const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(
-            base + (16 * kb + m16) * C::kKRow + (32 * st + 8 * g) * 2);
-        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[st], s[kb], 0, 0, 0);
+        const bf16x8_t a =
+            *reinterpret_cast<const bf16x8_t *>(kst + 32 * j * C::kRowB + koff[st]);
+        s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[st], s[j], 0, 0, 0);
       }
     }
-    if (t >= nfull) {  // diagonal tile: key position <= query position
+  };
+  // Causal mask (key position <= query position) and out-of-range spans.
+  auto mask = [&](int t, uint64_t badw, f32x16_t (&s)[KB]) __attribute__((always_inline)) {
+    const int lim = qpos - t * BN;  // last visible key of the lane's query
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+    for (int j = 0; j < KB; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (tile0 + 16 * kb + 4 * g + i > qpos32) s[kb][i] = -INFINITY;
+      for (int i = 0; i < 16; ++i) {
+        const int key = 32 * j + 8 * (i >> 2) + 4 * hh + (i & 3);
+        const bool dead = key > lim || ((badw >> (8 * (key >> 4))) & 1);
+        if (dead) s[j][i] = -INFINITY;
+      }
+  };
+  // Row max of a tile in base-2 units: chains of eight, then the lane pair.
+  auto tile_max = [&](const f32x16_t (&s)[KB]) __attribute__((always_inline)) -> float {
+    float mc[2 * KB];
+#pragma unroll
+    for (int c = 0; c < 2 * KB; ++c) {
+      const int j = c >> 1, b = 8 * (c & 1);
+      mc[c] = max3(s[j][b], s[j][b + 1], s[j][b + 2]);
+      mc[c] = max3(mc[c], s[j][b + 3], s[j][b + 4]);
+      mc[c] = max3(mc[c], s[j][b + 5], s[j][b + 6]);
+      mc[c] = __builtin_elementwise_maximum(mc[c], s[j][b + 7]);
     }
-    float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-      mx = fmaxf(fmaxf(mx, fmaxf(s[kb][0], s[kb][1])), fmaxf(s[kb][2], s[kb][3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_tile = mx * c2;
-    // Move the reference point only when the tile exceeds it by > kLazy.
+    for (int width = KB; width >= 1; width >>= 1)
+#pragma unroll
+      for (int c = 0; c < width; ++c) mc[c] = __builtin_elementwise_maximum(mc[c], mc[c + width]);
+    return pair_max(mc[0]) * c2;
+  };
+  // Moves the reference point when the tile max exceeds it by more than kLazy.
+  auto rescale = [&](float m_tile) __attribute__((always_inline)) {
     const bool move = m_tile > m_run + kLazy;
     if (__any(move)) {
       const float m_new = move ? m_tile : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 1 if kept
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 1 where kept
       l_run *= alpha;
 #pragma unroll
       for (int n = 0; n < NB; ++n) acc[n] *= alpha;
       m_run = m_new;
     }
-    float pr[KB][4];
-    float psum = 0.f;
+  };
+  // P = exp2(S*c2 - m) packed to bf16, FP32 row sums (four chains; FP32 adds
+  // issue alongside the MFMAs, v_dot2 would not), and O^T += V^T P^T.
+  auto attend = [&](const f32x16_t (&s)[KB], const unsigned char *vst) __attribute__((always_inline)) {
+    float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+    for (int j = 0; j < KB; ++j) {
+      uint32_t pk[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pr[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], c2, -m_run));
-        psum += pr[kb][i];
+      for (int x = 0; x < 8; ++x) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][2 * x], c2, -m_run));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][2 * x + 1], c2, -m_run));
+        pk[x] = bf16_pack2(p0, p1);
+        lsum[(2 * x) & 3] += p0;
+        lsum[(2 * x + 1) & 3] += p1;
       }
-    l_run += psum;
 #pragma unroll
-    for (int kp = 0; kp < KP; ++kp) {
-      const bf16x8_t pb = __builtin_bit_cast(
-          bf16x8_t,
-          make_uint4(bf16_pack2(pr[2 * kp][0], pr[2 * kp][1]),
-                     bf16_pack2(pr[2 * kp][2], pr[2 * kp][3]),
-                     bf16_pack2(pr[2 * kp + 1][0], pr[2 * kp + 1][1]),
-                     bf16_pack2(pr[2 * kp + 1][2], pr[2 * kp + 1][3])));
-      // A = V^T from the row-major V tile with ds_read_b64_tr_b16: in each
-      // 16-lane group, lane r points at V[kbase + r/4][dim0 + 4(r%4) .. +4)
-      // and lane i receives V[kbase + 0..3][dim0 + i] (kbase = 32kp + 4g,
-      // then +16 for slots 4..7; dim0 = 16n).
-      lds_t *vrow0 = (lds_t *)(base + C::kKBytes +
-                               (32 * kp + 4 * g + (m16 >> 2)) * C::kVRow + (m16 & 3) * 8);
+      for (int h16 = 0; h16 < 2; ++h16) {
+        const int kb = 2 * j + h16;  // 16-key block
+        const bf16x8_t pb = __builtin_bit_cast(
+            bf16x8_t, make_uint4(pk[4 * h16], pk[4 * h16 + 1], pk[4 * h16 + 2], pk[4 * h16 + 3]));
 #pragma unroll
-      for (int n = 0; n < NB; ++n) {
-        const s16x4_t lo =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vrow0 + 32 * n));
-        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4_t *)(vrow0 + 32 * n + 16 * C::kVRow));
-        const bf16x8_t a = __builtin_bit_cast(
-            bf16x8_t, make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
-                                 __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y));
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, acc[n], 0, 0, 0);
+        for (int n = 0; n < NB; ++n) {
+          const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t *)(vst + 16 * kb * C::kRowB + voff[0][n]));
+          const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t *)(vst + 16 * kb * C::kRowB + voff[1][n]));
+          const uint2 ulo = __builtin_bit_cast(uint2, lo), uhi = __builtin_bit_cast(uint2, hi);
+          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(ulo.x, ulo.y, uhi.x, uhi.y));
+          acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[n], 0, 0, 0);
+        }
       }
     }
+    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
   };
 
-  // Pipeline: block ids two tiles ahead, rows one tile ahead, LDS stage t % 2.
-  int64_t blk_next = ntiles > 1 ? block_of(1) : -1;
-  load_rows(0, block_of(0));
-  store_rows(0);
+  // Pipeline: block ids two tiles ahead, copies one tile ahead; the barrier
+  // after each step (which waits for this wave's copies) publishes the next
+  // stage. The loop is unrolled by two so each stage is a fixed LDS object.
+  // All splits run the same number of steps (an exhausted split idles).
+  int64_t ids[NSP], ids_next[NSP];
+  block_ids(t_lo, ids);
+  block_ids(t_lo + 1, ids_next);
+  if (t_lo < t_hi) {
+    issue(t_lo, ids, p.kc, ks0[split], badk0[split]);
+    issue(t_lo, ids, p.vc, vs0[split], nullptr);
+  }
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int64_t blk_after = t + 2 < ntiles ? block_of(t + 2) : -1;
-    if (t + 1 < ntiles) load_rows(t + 1, blk_next);
-    compute(t, t & 1);
-    if (t + 1 < ntiles) store_rows((t + 1) & 1);
+  auto step = [&](auto stage, int t) __attribute__((always_inline)) {
+    constexpr bool kEven = decltype(stage)::value == 0;
+    if (t + 1 < t_hi) {
+      issue(t + 1, ids_next, p.kc, kEven ? ks1[split] : ks0[split],
+            kEven ? badk1[split] : badk0[split]);
+      issue(t + 1, ids_next, p.vc, kEven ? vs1[split] : vs0[split], nullptr);
+      if (t + 2 < t_hi) block_ids(t + 2, ids_next);
+    }
+    if (t < wave_tiles) {
+      f32x16_t s[KB];
+      scores(kEven ? ks0[split] : ks1[split], s);
+      const uint64_t badw = read_bad(kEven ? badk0[split] : badk1[split]);
+      if (t >= wave_nfull || badw != 0) mask(t, badw, s);
+      rescale(tile_max(s));
+      attend(s, kEven ? vs0[split] : vs1[split]);
+    }
     __syncthreads();
-    blk_next = blk_after;
+  };
+  for (int s = 0; s < chunk; s += 2) {
+    step(std::integral_constant<int, 0>{}, t_lo + s);
+    if (s + 1 < chunk) step(std::integral_constant<int, 1>{}, t_lo + s + 1);
   }
 
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  if (q_ok) {
-    const float inv = 1.f / l_run;
-    uint16_t *orow = static_cast<uint16_t *>(p.out) + (r.q0 + qi) * p.o_st +
-                     (int64_t)h * p.o_sh;
+  if constexpr (KS > 1) {
+    // Splits 1.. hand (m, l, O^T) to split 0 through LDS, in a lane-major
+    // layout: word a of lane l of query group w at ((k-1)*4 + w)*A + a)*64 + l,
+    // laid over the stage objects in turn.
+    constexpr int A = 16 * NB + 2;
+    constexpr int kPer = static_cast<int>(sizeof(ks0) / sizeof(float));
+    static_assert(4 * sizeof(ks0) >= (KS - 1) * 4 * A * 64 * sizeof(float), "merge buffer");
+    auto xw = [&](int k, int a) __attribute__((always_inline)) -> float * {
+      const int idx = (((k - 1) * 4 + w) * A + a) * 64 + lane;
+      float *base = idx < kPer       ? reinterpret_cast<float *>(&ks0[0][0])
+                    : idx < 2 * kPer ? reinterpret_cast<float *>(&ks1[0][0])
+                    : idx < 3 * kPer ? reinterpret_cast<float *>(&vs0[0][0])
+                                     : reinterpret_cast<float *>(&vs1[0][0]);
+      return base + idx % kPer;
+    };
+    if (split > 0) {
 #pragma unroll
-    for (int n = 0; n < NB; ++n) {
-      // Lane l holds O[query][dims 16n + 4g + i].
-      const uint2 v = make_uint2(
-          (uint32_t)float_to_bf16_bits(acc[n][0] * inv) |
-              ((uint32_t)float_to_bf16_bits(acc[n][1] * inv) << 16),
-          (uint32_t)float_to_bf16_bits(acc[n][2] * inv) |
-              ((uint32_t)float_to_bf16_bits(acc[n][3] * inv) << 16));
-      *reinterpret_cast<uint2 *>(orow + 16 * n + 4 * g) = v;
+      for (int n = 0; n < NB; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) *xw(split, 16 * n + i) = acc[n][i];
+      *xw(split, 16 * NB) = m_run;
+      *xw(split, 16 * NB + 1) = l_run;
     }
+    __syncthreads();
+    if (split > 0) return;
+#pragma unroll
+    for (int k = 1; k < KS; ++k) {
+      const float m_o = *xw(k, 16 * NB), l_o = *xw(k, 16 * NB + 1);
+      const float m_new = __builtin_elementwise_maximum(m_run, m_o);
+      const float a_s = __builtin_amdgcn_exp2f(m_run - m_new);
+      const float a_o = __builtin_amdgcn_exp2f(m_o - m_new);
+      l_run = l_run * a_s + l_o * a_o;
+#pragma unroll
+      for (int n = 0; n < NB; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[n][i] = acc[n][i] * a_s + *xw(k, 16 * n + i) * a_o;
+      m_run = m_new;
+    }
+  }
+
+  const float l_tot = pair_sum(l_run);
+  if (q_ok) {
+    const float inv = 1.f / l_tot;
+    uint16_t *orow = static_cast<uint16_t *>(p.out) + (rg.q0 + qi) * p.o_st +
+                     static_cast<int64_t>(h) * p.o_sh;
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        // acc[n][4g4 + e] = O[query][32n + 8g4 + 4hh + e].
+        const f32x16_t &a = acc[n];
+        const uint2 v = make_uint2(
+            (uint32_t)float_to_bf16_bits(a[4 * g4] * inv) |
+                ((uint32_t)float_to_bf16_bits(a[4 * g4 + 1] * inv) << 16),
+            (uint32_t)float_to_bf16_bits(a[4 * g4 + 2] * inv) |
+                ((uint32_t)float_to_bf16_bits(a[4 * g4 + 3] * inv) << 16));
+        *reinterpret_cast<uint2 *>(orow + 32 * n + 8 * g4 + 4 * hh) = v;
+      }
   }
 }
 
-template <int D, int BN>
+template <int D, int BN, int KS>
 int launch(const PrefillParams &p, int64_t max_query_len, hipStream_t stream) {
-  using C = PrefillCfg<D, BN>;
-  const size_t lds = 2 * C::kStage;
-  dim3 grid(p.hq, p.num_seqs, static_cast<unsigned>(ceil_div(max_query_len, kBM)));
-  prefill_mfma<D, BN><<<grid, 256, lds, stream>>>(p);
+  PrefillParams q = p;
+  q.n_qtiles = static_cast<int>(ceil_div(max_query_len, kBM));
+  const int64_t blocks = static_cast<int64_t>(q.num_seqs) * q.n_qtiles * q.hq;
+  if (blocks > INT32_MAX)
+    return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_prefill: too many work items");
+  prefill_mfma<D, BN, KS><<<dim3(static_cast<unsigned>(blocks)), 256 * KS, 0, stream>>>(q);
   return check_launch("mlr_paged_prefill(mfma)");
 }
 
 }  // namespace
 
-bool prefill_mfma_eligible(int dtype, int64_t head_dim, int64_t block_size) {
-  (void)block_size;
-  return dtype == MLR_DTYPE_BF16 && (head_dim == 64 || head_dim == 128);
+bool prefill_mfma_eligible(const PrefillParams &p, int dtype) {
+  const bool aligned = (reinterpret_cast<uintptr_t>(p.q) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.kc) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.vc) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.out) & 7u) == 0 &&
+                       p.q_st % 8 == 0 && p.q_sh % 8 == 0 && p.o_st % 4 == 0 &&
+                       p.o_sh % 4 == 0;
+  // Positions are 32-bit inside the kernel; a 16-row span must fit a block.
+  return dtype == MLR_DTYPE_BF16 && (p.d == 64 || p.d == 128) && aligned &&
+         p.bs_log2 >= 4 && p.max_blocks * p.block_size < (int64_t(1) << 31) &&
+         p.scale > 0.0 && p.scale < 1e30;
 }
 
 int launch_prefill_mfma(const PrefillParams &p, int64_t max_query_len,
                         hipStream_t stream) {
-  if (max_query_len > int64_t(65535) * kBM)
-    return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_prefill: chunk too long");
   // The reference's tile_size only orders the FP32 accumulation; the kernel's
   // key tile is fixed per head_dim by its LDS budget.
-  if (p.d == 64) return launch<64, 64>(p, max_query_len, stream);
-  return launch<128, 32>(p, max_query_len, stream);
+  if (p.d == 64) return launch<64, 64, 2>(p, max_query_len, stream);
+  return launch<128, 64, 2>(p, max_query_len, stream);
 }
 
 }  // namespace mlr

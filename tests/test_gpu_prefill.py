@@ -6,6 +6,8 @@ Pools are NaN-filled outside the written context, so a stray read fails.
 
 from __future__ import annotations
 
+import itertools
+
 import pytest
 import torch
 
@@ -121,3 +123,92 @@ def test_varlen_equals_per_sequence_calls(device):
         single = kpa.paged_attention_prefill_chunk_tiled(
             wl.q[lo:hi].to(device), kc, vc, wl.tables[s], p, p + hi - lo, 16, 64)
         assert torch.equal(single, packed[lo:hi])
+
+
+# BF16 shapes at the edges of the matrix-core kernel's tiling: 32-query waves,
+# 128-query workgroups, 64-key tiles, 16-row copy spans and blocks larger
+# than a key tile.
+EDGE_CASES = [
+    # (hq, hkv, d, bs, prefix, chunk)
+    (14, 2, 64, 16, 0, 1),
+    (14, 2, 64, 16, 3, 31),
+    (8, 1, 64, 64, 64, 129),
+    (16, 2, 128, 256, 700, 300),
+    (8, 8, 128, 32, 1, 257),
+    (4, 2, 64, 128, 4095, 65),
+]
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs,prefix,chunk", EDGE_CASES,
+                         ids=[f"{c[0]}x{c[1]}-d{c[2]}-bs{c[3]}-p{c[4]}-c{c[5]}"
+                              for c in EDGE_CASES])
+def test_bf16_tiling_edges_match_oracle(device, hq, hkv, d, bs, prefix, chunk):
+    q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, torch.bfloat16,
+                                 seed=prefix + chunk)
+    want = opa.prefill_chunk_tiled(q, kc, vc, table, prefix, prefix + chunk, bs, 64)
+    got = kpa.paged_attention_prefill_chunk_tiled(
+        q.to(device), kc.to(device), vc.to(device), table, prefix, prefix + chunk, bs, 64)
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) <= 2e-2
+
+
+def test_bf16_ragged_varlen_matches_oracle(device):
+    """One launch over sequences of 1..300 queries with unrelated prefixes."""
+    hq, hkv, d, bs = 14, 2, 64, 16
+    qlens, prefixes = [1, 33, 128, 300, 7, 129], [0, 100, 5, 1000, 63, 2047]
+    gen = torch.Generator().manual_seed(11)
+    ctxs = [p + c for p, c in zip(prefixes, qlens)]
+    nblk = [(c + bs - 1) // bs for c in ctxs]
+    total_blocks = sum(nblk) + 3
+    perm = torch.randperm(total_blocks, generator=gen).tolist()
+    tables, at = [], 0
+    for n in nblk:
+        tables.append(perm[at:at + n])
+        at += n
+    kc = torch.full((total_blocks, bs, hkv, d), float("nan"), dtype=torch.bfloat16)
+    vc = torch.full_like(kc, float("nan"))
+    qs = []
+    for s, ctx in enumerate(ctxs):
+        k = torch.randn(ctx, hkv, d, generator=gen).to(torch.bfloat16)
+        v = torch.randn(ctx, hkv, d, generator=gen).to(torch.bfloat16)
+        for pos in range(ctx):
+            kc[tables[s][pos // bs], pos % bs] = k[pos]
+            vc[tables[s][pos // bs], pos % bs] = v[pos]
+        qs.append(torch.randn(qlens[s], hq, d, generator=gen).to(torch.bfloat16))
+    q = torch.cat(qs)
+    width = max(nblk)
+    bt = torch.tensor([t + [0] * (width - len(t)) for t in tables], dtype=torch.long)
+    qsl = torch.tensor([0] + list(itertools.accumulate(qlens)), dtype=torch.long)
+    got = kpa.paged_attention_prefill_varlen(
+        q.to(device), kc.to(device), vc.to(device), bt.to(device), qsl.to(device),
+        torch.tensor(ctxs, dtype=torch.long).to(device), bs, 64).cpu()
+    for s in range(len(qlens)):
+        lo, hi = int(qsl[s]), int(qsl[s + 1])
+        want = opa.prefill_chunk_tiled(q[lo:hi], kc, vc, tables[s], prefixes[s], ctxs[s], bs, 64)
+        assert max_abs(got[lo:hi], want) <= 2e-2, f"sequence {s}"
+
+
+@pytest.mark.parametrize("d,bs", [(64, 16), (128, 32), (40, 5)], ids=["d64", "d128", "generic"])
+def test_out_of_range_block_masks_its_tokens(device, d, bs):
+    """An out-of-range block id in the table hides that block's keys."""
+    from oracle import textbook
+    hq, hkv, prefix, chunk = 4, 2, 70, 40
+    q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, torch.bfloat16, seed=5)
+    bad_blk = 1  # a prefix block: its keys are visible to every query
+    context = prefix + chunk
+    visible = [[j <= prefix + i and j // bs != bad_blk for j in range(context)]
+               for i in range(chunk)]
+    want = torch.zeros(chunk, hq, d, dtype=torch.float64)
+    for h in range(hq):
+        k, v = textbook.logical_kv(kc.float().numpy(), vc.float().numpy(), table, context,
+                                   h // (hq // hkv))
+        want[:, h] = torch.from_numpy(textbook.attend(q[:, h].float().numpy(), k, v, visible))
+    broken = list(table)
+    broken[bad_blk] = kc.shape[0] + 7
+    bt = torch.tensor([broken], dtype=torch.long)
+    got = kpa.paged_prefill_launch(
+        q.to(device), kc.to(device), vc.to(device), bt.to(device),
+        torch.tensor([0, chunk], dtype=torch.long).to(device),
+        torch.tensor([context], dtype=torch.long).to(device), chunk).cpu()
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) <= 2e-2
