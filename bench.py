@@ -25,6 +25,11 @@ A secondary object reports BF16 chunk prefill (8 x 512-token chunks on
 prefixes U[0, 3584]) in TFLOP/s against the 2.5 PFLOP/s bf16 MFMA peak.
 
     python bench.py [--gpus 1] [--steps 240] [--warmup 48]
+
+``--profile`` launches the same kernels eagerly and untimed, for rocprofv3:
+``--steps`` decode steps over the rotated layers, the prefill call at each KV
+tile, and a plain 1 GiB device copy whose FETCH_SIZE / WRITE_SIZE counters
+calibrate the traffic counters (the copy reads and writes exactly 1 GiB).
 """
 
 from __future__ import annotations
@@ -58,6 +63,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--tokens-per-split", type=int, default=0)
+    p.add_argument("--profile", action="store_true",
+                   help="launch the kernels eagerly, untimed (for rocprofv3)")
     return p.parse_args()
 
 
@@ -78,6 +85,55 @@ def timed_graph(graph, replays, stream):
         stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / 1e3  # seconds
+
+
+def profile_run(args, device):
+    """Eager, untimed launches of the benchmarked kernels (for rocprofv3)."""
+    import torch
+
+    from mini_llm_runtime_amd import workloads
+    from mini_llm_runtime_amd.kernels import paged_attention as kpa
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+
+    wl = workloads.bf16_decode_qwen05b_b64()
+    nb = wl.k_cache.shape[0]
+    cache = PagedKVCache(LAYERS, nb, 16, 2, 64, dtype=torch.bfloat16, device=device)
+    for layer in range(LAYERS):
+        cache.k_cache[layer].copy_(wl.k_cache.to(device))
+        cache.v_cache[layer].copy_(wl.v_cache.to(device))
+    q, bt, ctx = wl.q.to(device), wl.block_tables.to(device), wl.context_lens.to(device)
+    slots, new_k, new_v = (t.to(device) for t in (wl.slot_mapping, wl.new_k, wl.new_v))
+    out = torch.empty_like(q)
+    ws = torch.empty(kpa.decode_workspace_bytes(64, 14, 64, bt.shape[1] * 16, torch.bfloat16),
+                     dtype=torch.uint8, device=device)
+    for i in range(args.steps):
+        k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
+        kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, workspace=ws, new_k=new_k,
+                                new_v=new_v, slot_mapping=slots)
+    torch.cuda.synchronize()
+    print(f"profile: {args.steps} decode steps", flush=True)
+    del cache
+    if not args.no_prefill:
+        pw = workloads.bf16_prefill_chunk512_x8()
+        kc, vc = pw.k_cache.clone(), pw.v_cache.clone()
+        kc.view(-1, 2, 64).index_copy_(0, pw.slot_mapping, pw.chunk_k)
+        vc.view(-1, 2, 64).index_copy_(0, pw.slot_mapping, pw.chunk_v)
+        kc, vc, pq = kc.to(device), vc.to(device), pw.q.to(device)
+        pbt, qsl, pctx = (t.to(device) for t in (pw.block_tables, pw.query_start_loc,
+                                                  pw.context_lens))
+        pout = torch.empty_like(pq)
+        for tile in (16, 64, 128):
+            for _ in range(5):
+                kpa.paged_prefill_launch(pq, kc, vc, pbt, qsl, pctx, 512, tile_size=tile,
+                                         out=pout)
+        torch.cuda.synchronize()
+        print("profile: 15 prefill calls", flush=True)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("profile: 3 copies of 1 GiB", flush=True)
 
 
 def bench_decode(args, device):
@@ -273,6 +329,17 @@ def cpu_baseline_prefill(wl, budget):
     }
 
 
+def measured_traffic():
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (profiles/traffic.json), or None when it is absent."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -283,6 +350,9 @@ def main():
     import torch
 
     device = torch.device("cuda", 0)
+    if args.profile:
+        profile_run(args, device)
+        return
     dec = bench_decode(args, device)
     pre = None if args.no_prefill else bench_prefill(device)
     cpu = None
@@ -291,6 +361,7 @@ def main():
         cpu = cpu_baseline_decode(dec["wl"], args.cpu_budget)
         if pre is not None:
             cpu_pre = cpu_baseline_prefill(pre["wl"], args.cpu_budget / 2)
+    traffic = measured_traffic()
     line = {
         "metric": METRIC,
         "value": round(dec["value_gbs"], 2),
@@ -317,13 +388,14 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": ("mlr_paged_decode_append (decode_split_mfma<64,4,false> with the "
-                       "KV write + decode_combine_mfma<64>)"),
+            "kernel": ("mlr_paged_decode_append (decode_split_mfma<64,4,false,true>, the "
+                       "split kernel with the KV write folded in, + decode_combine_mfma<64>)"),
             "achieved": round(dec["value_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["value_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic["decode_step_bytes"] if traffic else None,
+            "traffic_source": traffic["source"] if traffic else None,
             "algorithmic_bytes_per_launch": dec["step_bytes"],
             "avg_launch_us": round(dec["ms_per_step"] * 1e3, 3),
         },
@@ -337,7 +409,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 3),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 5),
-                         "traffic": None},
+                         "traffic": traffic["prefill_call_bytes"] if traffic else None},
             "flops_per_call": pre["flops_per_call"],
             "us_per_call_by_kv_tile": pre["us_per_call"],
             "cpu_baseline": cpu_pre,
