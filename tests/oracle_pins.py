@@ -176,3 +176,141 @@ def check_prefill_vs_textbook(mod):
 
 ALL_CHECKS = (check_decode_vs_kat, check_prefill_vs_kat, check_decode_vs_textbook,
               check_prefill_vs_textbook)
+
+
+# ---------------------------------------------------------------------------
+# Qwen2 attention callers (oracle/qwen2_attention.py) against float64 math
+# written out by hand: y = W h + b; RoPE as the rotation of each pair
+# (x_i, x_{i+D/2}) by angle position * theta^(-2i/D); textbook attention;
+# out = W_o . attention.
+# ---------------------------------------------------------------------------
+QWEN2_CFG = (4, 2, 8, 10000.0)  # Hq, Hkv, D, rope theta
+
+
+def qwen2_weights(seed=0, dtype=torch.float64):
+    hq, hkv, d, _ = QWEN2_CFG
+    hidden = hq * d
+    gen = torch.Generator().manual_seed(seed)
+    rnd = lambda *s: (torch.randn(*s, generator=gen) * 0.3).to(dtype)
+    return {"q_w": rnd(hq * d, hidden), "q_b": rnd(hq * d), "k_w": rnd(hkv * d, hidden),
+            "k_b": rnd(hkv * d), "v_w": rnd(hkv * d, hidden), "v_b": rnd(hkv * d),
+            "o_w": rnd(hidden, hidden)}
+
+
+def _np_rope(x, pos, theta):
+    """x [heads, D] at integer position pos, pair rotation."""
+    d = x.shape[-1]
+    half = d // 2
+    out = np.empty_like(x)
+    for i in range(half):
+        ang = pos * theta ** (-2.0 * i / d)
+        c, s = np.cos(ang), np.sin(ang)
+        out[:, i] = x[:, i] * c - x[:, i + half] * s
+        out[:, i + half] = x[:, i + half] * c + x[:, i] * s
+    return out
+
+
+def _np_qkv(h, w, pos):
+    hq, hkv, d, theta = QWEN2_CFG
+    wn = {k: v.numpy() for k, v in w.items()}
+    q = (wn["q_w"] @ h + wn["q_b"]).reshape(hq, d)
+    k = (wn["k_w"] @ h + wn["k_b"]).reshape(hkv, d)
+    v = (wn["v_w"] @ h + wn["v_b"]).reshape(hkv, d)
+    return _np_rope(q, pos, theta), _np_rope(k, pos, theta), v
+
+
+def _np_attend(q, keys, values, nvis):
+    """q [Hq, D] over the first nvis keys [N, Hkv, D] -> [Hq*D]."""
+    hq, hkv, d, _ = QWEN2_CFG
+    group = hq // hkv
+    rows = []
+    for h in range(hq):
+        rows.append(textbook.attend(q[h][None], keys[:nvis, h // group], values[:nvis, h // group],
+                                    np.ones((1, nvis), bool))[0])
+    return np.concatenate(rows)
+
+
+def check_qwen2_callers_vs_textbook(mod):
+    # Tolerance 1e-6: the reference builds the RoPE cos/sin tables in FP32
+    # (model/qwen2.py:160-170) even for FP64 activations, the textbook here
+    # in FP64.
+    hq, hkv, d, theta = QWEN2_CFG
+    from oracle.paged_kv_cache import OracleKVCache
+    w = qwen2_weights()
+    wo = w["o_w"].numpy()
+    gen = torch.Generator().manual_seed(7)
+    bs, nblocks = 4, 24
+    perm = torch.randperm(nblocks, generator=gen).tolist()
+    # Logical K/V history of three sequences (positions before their new token).
+    lens = [5, 11, 2]
+    tables = [perm[0:2], perm[2:5], perm[5:6]]
+    hist_k = [torch.randn(n, hkv, d, generator=gen, dtype=torch.float64) for n in lens]
+    hist_v = [torch.randn(n, hkv, d, generator=gen, dtype=torch.float64) for n in lens]
+
+    def fresh_cache():
+        cache = OracleKVCache(1, nblocks, bs, hkv, d, dtype=torch.float64)
+        cache.k_cache.fill_(1e3)
+        cache.v_cache.fill_(1e3)
+        for s, n in enumerate(lens):
+            for p in range(n):
+                cache.k_cache[0, tables[s][p // bs], p % bs] = hist_k[s][p]
+                cache.v_cache[0, tables[s][p // bs], p % bs] = hist_v[s][p]
+        return cache
+
+    # Batched decode: the new token sits at position len (context len + 1).
+    hidden = torch.randn(3, 1, hq * d, generator=gen, dtype=torch.float64)
+    ctx = torch.tensor([n + 1 for n in lens])
+    pos = (ctx - 1).unsqueeze(1)
+    width = max(len(t) for t in tables)
+    bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables])
+    slots = torch.tensor([tables[s][n // bs] * bs + n % bs for s, n in enumerate(lens)])
+    cache = fresh_cache()
+    got = mod.decode_batch(hidden, pos, cache, 0, slots, bt, ctx, w, QWEN2_CFG)
+    for s, n in enumerate(lens):
+        q, k, v = _np_qkv(hidden[s, 0].numpy(), w, n)
+        keys = np.concatenate([hist_k[s].numpy(), k[None]])
+        vals = np.concatenate([hist_v[s].numpy(), v[None]])
+        want = wo @ _np_attend(q, keys, vals, n + 1)
+        np.testing.assert_allclose(got[s, 0].numpy(), want, rtol=1e-6, atol=1e-6)
+        single_cache = fresh_cache()
+        one = mod.decode_single(hidden[s:s + 1], pos[s:s + 1], single_cache, 0, slots[s:s + 1],
+                                tables[s], n + 1, w, QWEN2_CFG)
+        np.testing.assert_allclose(one[0, 0].numpy(), want, rtol=1e-6, atol=1e-6)
+
+    # Chunk prefill of sequence 1: three new tokens after its 11-token prefix.
+    prefix, chunk = lens[1], 3
+    table = perm[2:6]  # room for 14 positions
+    hidden = torch.randn(1, chunk, hq * d, generator=gen, dtype=torch.float64)
+    positions = torch.arange(prefix, prefix + chunk).unsqueeze(0)
+    cslots = torch.tensor([table[p // bs] * bs + p % bs for p in range(prefix, prefix + chunk)])
+    cache = fresh_cache()
+    got = mod.prefill_chunk(hidden, positions, cache, 0, cslots, table, prefix, prefix + chunk,
+                            2, w, QWEN2_CFG)
+    new = [_np_qkv(hidden[0, i].numpy(), w, prefix + i) for i in range(chunk)]
+    keys = np.concatenate([hist_k[1].numpy(), np.stack([n[1] for n in new])])
+    vals = np.concatenate([hist_v[1].numpy(), np.stack([n[2] for n in new])])
+    for i in range(chunk):
+        want = wo @ _np_attend(new[i][0], keys, vals, prefix + i + 1)
+        np.testing.assert_allclose(got[0, i].numpy(), want, rtol=1e-6, atol=1e-6)
+
+    # Whole-prompt prefill: five tokens at positions 0..4, causal.
+    hidden = torch.randn(1, 5, hq * d, generator=gen, dtype=torch.float64)
+    positions = torch.arange(5).unsqueeze(0)
+    pslots = torch.tensor([perm[10] * bs + p if p < bs else perm[11] * bs + p - bs
+                           for p in range(5)])
+    cache = fresh_cache()
+    got = mod.prefill_whole(hidden, positions, cache, 0, pslots, w, QWEN2_CFG)
+    new = [_np_qkv(hidden[0, i].numpy(), w, i) for i in range(5)]
+    keys = np.stack([n[1] for n in new])
+    vals = np.stack([n[2] for n in new])
+    for i in range(5):
+        want = wo @ _np_attend(new[i][0], keys, vals, i + 1)
+        np.testing.assert_allclose(got[0, i].numpy(), want, rtol=1e-6, atol=1e-6)
+    # The prompt's rows landed in their slots.
+    for p in range(5):
+        slot = int(pslots[p])
+        np.testing.assert_allclose(cache.k_cache[0, slot // bs, slot % bs].numpy(), new[p][1],
+                                   rtol=1e-6, atol=1e-6)
+
+
+QWEN2_CHECKS = (check_qwen2_callers_vs_textbook,)

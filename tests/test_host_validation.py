@@ -142,3 +142,87 @@ def test_chunk_prefill_validation_messages():
                                                 9, 3, 4)
     with pytest.raises(RuntimeError, match="only on HIP devices"):
         kpa.paged_attention_prefill_chunk_tiled(q, k, v, [2, 0, 3], 5, 9, 3, 4)
+
+
+def _tiny_attention():
+    import types
+
+    from mini_llm_runtime_amd.model.qwen2_attention import Qwen2Attention
+    cfg = types.SimpleNamespace(hidden_size=32, num_attention_heads=4, num_key_value_heads=2,
+                                head_dim=8, rope_theta=10_000.0)
+    torch.manual_seed(0)
+    return Qwen2Attention(cfg), cfg
+
+
+@pytest.mark.parametrize("mutate,message", [
+    (lambda a: a.update(context_lens=torch.tensor([0, 6])), "context_lens must be greater than 0"),
+    (lambda a: a.update(position_ids=torch.tensor([[3], [5]])),
+     "decode positions must equal context_lens - 1"),
+    (lambda a: a.update(block_tables=torch.tensor([[1], [2]]), context_lens=torch.tensor([5, 6]),
+                        position_ids=torch.tensor([[4], [5]])),
+     "block_tables have insufficient blocks for context_lens"),
+    (lambda a: a.update(block_tables=torch.tensor([[1, 99], [2, 3]])),
+     "block_tables contain an invalid physical block"),
+    (lambda a: a.update(slot_mapping=torch.tensor([4 * 1 + 1, 3 * 4 + 1])),
+     "slot_mapping must match block_tables and positions"),
+    (lambda a: a.update(slot_mapping=torch.tensor([5, 5]), block_tables=torch.tensor([[1, 1], [1, 1]]),
+                        position_ids=torch.tensor([[5], [5]]), context_lens=torch.tensor([6, 6])),
+     "decode requests must use distinct write slots"),
+])
+def test_qwen2_decode_batch_validation_messages(mutate, message):
+    """Reference model/qwen2.py:578-602: each check raises its message before
+    anything is written (one host sync evaluates them all)."""
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+    attn, cfg = _tiny_attention()
+    cache = PagedKVCache(1, 8, 4, 2, 8, dtype=torch.float32)
+    cache.k_cache.zero_()
+    before = cache.k_cache.clone()
+    args = dict(position_ids=torch.tensor([[4], [5]]), slot_mapping=torch.tensor([4 * 2 + 0, 4 * 3 + 1]),
+                block_tables=torch.tensor([[1, 2], [2, 3]]), context_lens=torch.tensor([5, 6]))
+    mutate(args)
+    with pytest.raises(ValueError, match=message):
+        attn.forward_decode_batch_with_cache(torch.zeros(2, 1, cfg.hidden_size), args["position_ids"],
+                                             cache, 0, args["slot_mapping"], args["block_tables"],
+                                             args["context_lens"])
+    assert torch.equal(cache.k_cache, before)
+
+
+def test_qwen2_decode_batch_valid_call_refuses_cpu():
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+    attn, cfg = _tiny_attention()
+    cache = PagedKVCache(1, 8, 4, 2, 8, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="HIP"):
+        attn.forward_decode_batch_with_cache(
+            torch.zeros(2, 1, cfg.hidden_size), torch.tensor([[4], [5]]), cache, 0,
+            torch.tensor([4 * 2 + 0, 4 * 3 + 1]), torch.tensor([[1, 2], [2, 3]]),
+            torch.tensor([5, 6]))
+
+
+@pytest.mark.parametrize("kwargs,message", [
+    (dict(prefix_len=-1, context_len=2), "prefix_len cannot be negative"),
+    (dict(prefix_len=0, context_len=5), "context_len must equal prefix_len"),
+    (dict(prefix_len=0, context_len=3, tile_size=0), "tile_size must be greater than 0"),
+    (dict(prefix_len=0, context_len=3, positions=[[1, 2, 3]]), "contiguous global positions"),
+    (dict(prefix_len=0, context_len=3, table=[]), "enough blocks"),
+    (dict(prefix_len=0, context_len=3, table=[42]), "out-of-range physical block"),
+    (dict(prefix_len=0, context_len=3, slots=[5, 6, 7]), "slot_mapping does not match"),
+])
+def test_qwen2_chunk_prefill_validation_messages(kwargs, message):
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+    attn, cfg = _tiny_attention()
+    cache = PagedKVCache(1, 8, 4, 2, 8, dtype=torch.float32)
+    table = kwargs.get("table", [3])
+    positions = torch.tensor(kwargs.get("positions", [[0, 1, 2]]))
+    slots = torch.tensor(kwargs.get("slots", [12, 13, 14]))
+    with pytest.raises(ValueError, match=message):
+        attn.forward_prefill_chunk_with_cache(
+            torch.zeros(1, 3, cfg.hidden_size), positions, cache, 0, slots, table,
+            kwargs["prefix_len"], kwargs["context_len"], kwargs.get("tile_size", 4))
+
+
+def test_qwen2_attention_matches_reference_state_dict_names():
+    attn, _ = _tiny_attention()
+    assert list(attn.state_dict()) == [
+        "qkv_proj.q_proj.weight", "qkv_proj.q_proj.bias", "qkv_proj.v_proj.weight",
+        "qkv_proj.v_proj.bias", "qkv_proj.k_proj.weight", "qkv_proj.k_proj.bias",
+        "o_proj.weight"]

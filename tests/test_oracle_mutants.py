@@ -76,3 +76,42 @@ def test_pins_catch_planted_mistake(name):
         except (AssertionError, IndexError, RuntimeError, ValueError):
             caught.append(check.__name__)
     assert caught, f"no pin detects the planted mistake {name!r}"
+
+
+# The same for the Qwen2 attention callers (oracle/qwen2_attention.py).
+QWEN2_MUTATIONS = {
+    "rope-sign-flipped": (
+        "turned = torch.cat((-x[..., half:], x[..., :half]), dim=-1)",
+        "turned = torch.cat((x[..., half:], -x[..., :half]), dim=-1)",
+    ),
+    "rope-adjacent-pairs": (
+        "turned = torch.cat((-x[..., half:], x[..., :half]), dim=-1)",
+        "turned = torch.stack((-x[..., 1::2], x[..., ::2]), dim=-1).flatten(-2)",
+    ),
+    "rope-angles-not-duplicated": (
+        "angles = torch.cat((angles, angles), dim=-1)",
+        "angles = torch.cat((angles, angles.flip(-1)), dim=-1)",
+    ),
+    "k-bias-dropped": (
+        'k = torch.nn.functional.linear(hidden, w["k_w"], w["k_b"])',
+        'k = torch.nn.functional.linear(hidden, w["k_w"])',
+    ),
+}
+
+
+@pytest.mark.parametrize("name", sorted(QWEN2_MUTATIONS))
+def test_qwen2_pins_catch_planted_mistake(name):
+    import oracle.qwen2_attention as qa
+    before, after = QWEN2_MUTATIONS[name]
+    source = inspect.getsource(qa)
+    assert source.count(before) == 1, f"mutation site for {name} not found exactly once"
+    module = types.ModuleType(f"oracle.qwen2_mutant_{name.replace('-', '_')}")
+    module.__package__ = "oracle"
+    exec(compile(source.replace(before, after), module.__name__, "exec"), module.__dict__)
+    caught = []
+    for check in oracle_pins.QWEN2_CHECKS:
+        try:
+            check(module)
+        except (AssertionError, IndexError, RuntimeError, ValueError):
+            caught.append(check.__name__)
+    assert caught, f"no pin detects the planted mistake {name!r}"

@@ -12,6 +12,12 @@ from oracle.slots import pad_block_tables, slots_for_positions
 import oracle_pins
 
 
+@pytest.mark.parametrize("check", oracle_pins.QWEN2_CHECKS, ids=lambda c: c.__name__)
+def test_oracle_qwen2_callers_are_pinned(check):
+    import oracle.qwen2_attention as qa
+    check(qa)
+
+
 @pytest.mark.parametrize("check", oracle_pins.ALL_CHECKS, ids=lambda c: c.__name__)
 def test_oracle_attention_is_pinned(check):
     check(pa)
