@@ -425,14 +425,17 @@ __global__ __launch_bounds__(64) void decode_combine_mfma(DecodeParams p) {
   float den = 0.f, M = -INFINITY;
   for (int s0 = 0; s0 < ns; s0 += kChunk) {
     const int cnt = min(kChunk, ns - s0);
+    // Unconditional loads (splits past cnt repeat the last one, weight 0): a
+    // load under a per-split branch would wait for the one before it.
     float a[kChunk][C];
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
+      const int jc = j < cnt ? j : cnt - 1;
 #pragma unroll
-      for (int c = 0; c < C; ++c)
-        a[j][c] = j < cnt ? ws_acc[(row0 + s0 + j) * D + 64 * c + lane] : 0.f;
+      for (int c = 0; c < C; ++c) a[j][c] = ws_acc[(row0 + s0 + jc) * D + 64 * c + lane];
     }
-    const float2 ml = lane < cnt ? p.ws_ml[row0 + s0 + lane] : make_float2(-INFINITY, 0.f);
+    const float2 ml_raw = p.ws_ml[row0 + s0 + (lane < cnt ? lane : 0)];
+    const float2 ml = lane < cnt ? ml_raw : make_float2(-INFINITY, 0.f);
     const float m_new = fmaxf(M, wave_max(ml.x));
     const float rescale = __builtin_amdgcn_exp2f(M - m_new);  // 0 on the first chunk
     const float f = __builtin_amdgcn_exp2f(ml.x - m_new);

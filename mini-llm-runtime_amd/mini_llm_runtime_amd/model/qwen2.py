@@ -1,0 +1,419 @@
+"""Qwen2 causal LM around the MI355X paged attention (reference
+model/qwen2.py:14-123, 768-1240).
+
+The modules, their names and construction order follow the reference, so a
+reference state_dict loads unchanged and a seeded construction draws the same
+random weights: ``TinyQwen2ForCausalLM`` = ``TinyQwen2Model`` (embed_tokens,
+layers of ``Qwen2DecoderLayer``, norm) + lm_head (tied to the embedding when
+the config says so). Each layer is pre-norm attention + pre-norm SwiGLU MLP
+with residuals; RMSNorm keeps FP32 statistics for half-precision inputs.
+
+The attention is ``Qwen2Attention`` on the HIP kernels. Besides the
+reference's entry points, the model has ``forward_prefill_packed_with_cache``:
+the prompts (or prompt chunks) of several requests in one packed forward,
+which the runner uses for every prefill of a step.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, fields
+from typing import Any
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ..runtime.paged_kv_cache import PagedKVCache
+from .qwen2_attention import Qwen2Attention, _raise_first
+
+
+@dataclass(frozen=True)
+class TinyQwen2Config:
+    vocab_size: int = 128
+    hidden_size: int = 64
+    intermediate_size: int = 128
+    num_hidden_layers: int = 2
+    num_attention_heads: int = 4
+    num_key_value_heads: int = 2
+    max_position_embeddings: int = 128
+    rope_theta: float = 1_000_000.0
+    rms_norm_eps: float = 1e-6
+    tie_word_embeddings: bool = False
+    bos_token_id: int | None = None
+    eos_token_id: int | None = None
+
+    @classmethod
+    def from_dict(cls, config_dict: dict[str, Any]) -> "TinyQwen2Config":
+        """Build from a HF-style config dict, ignoring keys it does not know."""
+        known = {f.name for f in fields(cls)}
+        return cls(**{k: v for k, v in config_dict.items() if k in known})
+
+    def __post_init__(self) -> None:
+        for name in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers",
+                     "num_attention_heads", "num_key_value_heads",
+                     "max_position_embeddings"):
+            if getattr(self, name) <= 0:
+                raise ValueError(f"{name} must be greater than 0")
+        if self.rope_theta <= 0:
+            raise ValueError("rope_theta must be greater than 0")
+        if self.rms_norm_eps <= 0:
+            raise ValueError("rms_norm_eps must be greater than 0")
+        if self.hidden_size % self.num_attention_heads != 0:
+            raise ValueError("hidden_size must be divisible by num_attention_heads")
+        if self.num_attention_heads % self.num_key_value_heads != 0:
+            raise ValueError("num_attention_heads must be divisible by num_key_value_heads")
+        if self.head_dim % 2 != 0:
+            raise ValueError("head_dim must be even for rotary embeddings")
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+
+class Qwen2RMSNorm(nn.Module):
+    """x / sqrt(mean(x^2) + eps) * weight; statistics in FP32 for FP16/BF16
+    inputs, and the product taken in the input dtype (reference :88-123)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        if hidden_size <= 0:
+            raise ValueError("hidden_size must be greater than 0")
+        if eps <= 0:
+            raise ValueError("eps must be greater than 0")
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.variance_epsilon = eps
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        if hidden_states.shape[-1] != self.weight.shape[0]:
+            raise ValueError("hidden_states last dimension must match hidden_size "
+                             f"({self.weight.shape[0]}), got {hidden_states.shape[-1]}")
+        dtype = hidden_states.dtype
+        stats = torch.float32 if dtype in (torch.float16, torch.bfloat16) else dtype
+        x = hidden_states.to(stats)
+        normalized = x * torch.rsqrt(x.square().mean(dim=-1, keepdim=True)
+                                     + self.variance_epsilon)
+        return self.weight.to(dtype) * normalized.to(dtype)
+
+
+class Qwen2MLP(nn.Module):
+    """down(silu(gate(x)) * up(x)) (reference :768-792)."""
+
+    def __init__(self, config: TinyQwen2Config) -> None:
+        super().__init__()
+        self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(hidden_states)) * self.up_proj(hidden_states))
+
+
+class Qwen2DecoderLayer(nn.Module):
+    """Pre-norm attention and MLP blocks with residuals (reference :794-940)."""
+
+    def __init__(self, config: TinyQwen2Config) -> None:
+        super().__init__()
+        self.self_attn = Qwen2Attention(config)
+        self.mlp = Qwen2MLP(config)
+        self.input_layernorm = Qwen2RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = Qwen2RMSNorm(config.hidden_size,
+                                                     eps=config.rms_norm_eps)
+
+    def _block(self, hidden_states: torch.Tensor, attend) -> torch.Tensor:
+        hidden_states = hidden_states + attend(self.input_layernorm(hidden_states))
+        return hidden_states + self.mlp(self.post_attention_layernorm(hidden_states))
+
+    def forward(self, hidden_states: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
+        return self._block(hidden_states, lambda h: self.self_attn(h, position_ids))
+
+    def forward_prefill_with_cache(self, hidden_states, position_ids, kv_cache, layer_idx,
+                                   slot_mapping) -> torch.Tensor:
+        return self._block(hidden_states, lambda h: self.self_attn.forward_prefill_with_cache(
+            hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+            layer_idx=layer_idx, slot_mapping=slot_mapping))
+
+    def forward_decode_with_cache(self, hidden_states, position_ids, kv_cache, layer_idx,
+                                  slot_mapping, block_table, context_len) -> torch.Tensor:
+        return self._block(hidden_states, lambda h: self.self_attn.forward_decode_with_cache(
+            hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+            layer_idx=layer_idx, slot_mapping=slot_mapping, block_table=block_table,
+            context_len=context_len))
+
+    def forward_decode_batch_with_cache(self, hidden_states, position_ids, kv_cache,
+                                        layer_idx, slot_mapping, block_tables,
+                                        context_lens) -> torch.Tensor:
+        return self._block(
+            hidden_states, lambda h: self.self_attn.forward_decode_batch_with_cache(
+                hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+                layer_idx=layer_idx, slot_mapping=slot_mapping, block_tables=block_tables,
+                context_lens=context_lens))
+
+    def forward_prefill_packed_with_cache(self, hidden_states, position_ids, kv_cache,
+                                          layer_idx, slot_mapping, block_tables,
+                                          query_start_loc, context_lens,
+                                          max_query_len) -> torch.Tensor:
+        return self._block(
+            hidden_states, lambda h: self.self_attn.forward_prefill_packed_with_cache(
+                hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+                layer_idx=layer_idx, slot_mapping=slot_mapping, block_tables=block_tables,
+                query_start_loc=query_start_loc, context_lens=context_lens,
+                max_query_len=max_query_len))
+
+
+class TinyQwen2Model(nn.Module):
+    """Embedding, decoder layers and the final norm (reference :943-1167)."""
+
+    def __init__(self, config: TinyQwen2Config) -> None:
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList(
+            [Qwen2DecoderLayer(config) for _ in range(config.num_hidden_layers)])
+        self.norm = Qwen2RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    # Shared argument checks -------------------------------------------------
+    @staticmethod
+    def _check_ids(input_ids: torch.Tensor) -> None:
+        if input_ids.dtype not in (torch.int32, torch.int64):
+            raise TypeError("input_ids must have dtype torch.int32 or torch.int64, "
+                            f"got {input_ids.dtype}")
+
+    def _check_cache(self, kv_cache: PagedKVCache) -> None:
+        if kv_cache.num_layers != len(self.layers):
+            raise ValueError("KV cache num_layers must match model layers "
+                             f"({len(self.layers)}), got {kv_cache.num_layers}")
+        if kv_cache.num_kv_heads != self.config.num_key_value_heads:
+            raise ValueError("KV cache num_kv_heads must match model num_key_value_heads "
+                             f"({self.config.num_key_value_heads}), "
+                             f"got {kv_cache.num_kv_heads}")
+        if kv_cache.head_dim != self.config.head_dim:
+            raise ValueError("KV cache head_dim must match model head_dim "
+                             f"({self.config.head_dim}), got {kv_cache.head_dim}")
+
+    def _run(self, input_ids: torch.Tensor, step) -> torch.Tensor:
+        hidden_states = self.embed_tokens(input_ids)
+        for layer_idx, layer in enumerate(self.layers):
+            hidden_states = step(layer, layer_idx, hidden_states)
+        return self.norm(hidden_states)
+
+    # Entry points -----------------------------------------------------------
+    def forward(self, input_ids: torch.Tensor,
+                position_ids: torch.Tensor | None = None) -> torch.Tensor:
+        if input_ids.ndim != 2:
+            raise ValueError("input_ids must have shape [batch_size, seq_len], "
+                             f"got {tuple(input_ids.shape)}")
+        self._check_ids(input_ids)
+        batch_size, seq_len = input_ids.shape
+        if seq_len == 0:
+            raise ValueError("input_ids sequence length must be greater than 0")
+        if position_ids is None:
+            position_ids = torch.arange(seq_len, dtype=torch.long,
+                                        device=input_ids.device).expand(batch_size, -1)
+        elif position_ids.shape != input_ids.shape:
+            raise ValueError("position_ids shape must match input_ids shape "
+                             f"{tuple(input_ids.shape)}, got {tuple(position_ids.shape)}")
+        return self._run(input_ids, lambda layer, i, h: layer(h, position_ids))
+
+    def forward_prefill_with_cache(self, input_ids, position_ids, kv_cache,
+                                   slot_mapping) -> torch.Tensor:
+        if input_ids.ndim != 2:
+            raise ValueError("input_ids must have shape [1, seq_len], "
+                             f"got {tuple(input_ids.shape)}")
+        if input_ids.shape[0] != 1:
+            raise ValueError("prefill with cache currently supports exactly one request, "
+                             f"got batch_size={input_ids.shape[0]}")
+        if input_ids.shape[1] == 0:
+            raise ValueError("input_ids sequence length must be greater than 0")
+        self._check_ids(input_ids)
+        if position_ids.shape != input_ids.shape:
+            raise ValueError("position_ids shape must match input_ids shape "
+                             f"{tuple(input_ids.shape)}, got {tuple(position_ids.shape)}")
+        if slot_mapping.ndim != 1:
+            raise ValueError("slot_mapping must have shape [seq_len], "
+                             f"got {tuple(slot_mapping.shape)}")
+        if slot_mapping.shape[0] != input_ids.shape[1]:
+            raise ValueError("slot_mapping length must match sequence length "
+                             f"({input_ids.shape[1]}), got {slot_mapping.shape[0]}")
+        self._check_cache(kv_cache)
+        return self._run(input_ids, lambda layer, i, h: layer.forward_prefill_with_cache(
+            h, position_ids, kv_cache, i, slot_mapping))
+
+    def forward_decode_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
+                                  block_table, context_len) -> torch.Tensor:
+        if input_ids.ndim != 2:
+            raise ValueError("input_ids must have shape [1, 1] for decode, "
+                             f"got {tuple(input_ids.shape)}")
+        if tuple(input_ids.shape) != (1, 1):
+            raise ValueError("decode with cache requires exactly one request and one token, "
+                             f"got {tuple(input_ids.shape)}")
+        self._check_ids(input_ids)
+        if position_ids.shape != input_ids.shape:
+            raise ValueError("position_ids shape must match input_ids shape "
+                             f"{tuple(input_ids.shape)}, got {tuple(position_ids.shape)}")
+        if slot_mapping.ndim != 1 or slot_mapping.shape[0] != 1:
+            raise ValueError("slot_mapping must have shape [1] for decode, "
+                             f"got {tuple(slot_mapping.shape)}")
+        if context_len <= 0:
+            raise ValueError("context_len must be greater than 0")
+        position = int(position_ids.item())
+        if position != context_len - 1:
+            raise ValueError("decode position must equal context_len - 1, "
+                             f"got position={position} and context_len={context_len}")
+        if len(block_table) < -(-context_len // kv_cache.block_size):
+            raise ValueError("block_table does not contain enough blocks for context_len")
+        self._check_cache(kv_cache)
+        return self._run(input_ids, lambda layer, i, h: layer.forward_decode_with_cache(
+            h, position_ids, kv_cache, i, slot_mapping, block_table, context_len))
+
+    def forward_decode_batch_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
+                                        block_tables, context_lens) -> torch.Tensor:
+        """[B, 1] token ids -> [B, 1, hidden_size]."""
+        if input_ids.ndim != 2 or input_ids.shape[1] != 1:
+            raise ValueError("input_ids must have shape [B, 1] for decode")
+        if input_ids.shape[0] == 0:
+            raise ValueError("decode batch must not be empty")
+        if input_ids.dtype not in (torch.int32, torch.int64):
+            raise TypeError("input_ids must have dtype torch.int32 or torch.int64")
+        if position_ids.shape != input_ids.shape:
+            raise ValueError("position_ids shape must match input_ids shape")
+        if input_ids.device != self.embed_tokens.weight.device:
+            raise ValueError("input_ids and model must be on the same device")
+        if kv_cache.num_layers != len(self.layers):
+            raise ValueError("KV cache num_layers must match model layers")
+        if kv_cache.num_kv_heads != self.config.num_key_value_heads:
+            raise ValueError("KV cache num_kv_heads must match model num_key_value_heads")
+        if kv_cache.head_dim != self.config.head_dim:
+            raise ValueError("KV cache head_dim must match model head_dim")
+        return self._run(input_ids, lambda layer, i, h: layer.forward_decode_batch_with_cache(
+            h, position_ids, kv_cache, i, slot_mapping, block_tables, context_lens))
+
+    def forward_prefill_packed_with_cache(self, input_ids: torch.Tensor,
+                                          position_ids: torch.Tensor,
+                                          kv_cache: PagedKVCache,
+                                          slot_mapping: torch.Tensor,
+                                          block_tables: torch.Tensor,
+                                          query_start_loc: torch.Tensor,
+                                          context_lens: torch.Tensor,
+                                          max_query_len: int) -> torch.Tensor:
+        """Packed prefill of R requests: [T] token ids -> [T, hidden_size].
+
+        Request r owns tokens query_start_loc[r]:query_start_loc[r+1]
+        (non-empty), at positions context_lens[r] - len_r .. context_lens[r] - 1
+        of its block table (a whole prompt when the prefix is 0, else a chunk
+        after a cached prefix). The metadata is checked once here, on the
+        device with one host sync, before any layer writes the cache."""
+        if input_ids.ndim != 1 or input_ids.shape[0] == 0:
+            raise ValueError("input_ids must have shape [num_tokens] with num_tokens > 0")
+        self._check_ids(input_ids)
+        for name, tensor in (("position_ids", position_ids), ("slot_mapping", slot_mapping)):
+            if tensor.shape != input_ids.shape:
+                raise ValueError(f"{name} must have the shape of input_ids")
+        num_requests = context_lens.shape[0]
+        if context_lens.ndim != 1 or num_requests == 0:
+            raise ValueError("context_lens must have shape [num_requests]")
+        if query_start_loc.shape != (num_requests + 1,):
+            raise ValueError("query_start_loc must have num_requests + 1 entries")
+        if block_tables.ndim != 2 or block_tables.shape[0] != num_requests:
+            raise ValueError("block_tables must have shape [num_requests, max_num_blocks]")
+        for name, tensor in (("position_ids", position_ids), ("slot_mapping", slot_mapping),
+                             ("block_tables", block_tables),
+                             ("query_start_loc", query_start_loc),
+                             ("context_lens", context_lens)):
+            if tensor.dtype != torch.long:
+                raise ValueError(f"{name} must use torch.long dtype")
+            if tensor.device != input_ids.device:
+                raise ValueError(f"{name} must be on the same device as input_ids")
+        self._check_cache(kv_cache)
+        self._check_packed_metadata(kv_cache, position_ids, slot_mapping, block_tables,
+                                    query_start_loc, context_lens, max_query_len,
+                                    input_ids.shape[0])
+        hidden_states = self.embed_tokens(input_ids)
+        for layer_idx, layer in enumerate(self.layers):
+            hidden_states = layer.forward_prefill_packed_with_cache(
+                hidden_states, position_ids, kv_cache, layer_idx, slot_mapping, block_tables,
+                query_start_loc, context_lens, max_query_len)
+        return self.norm(hidden_states)
+
+    @staticmethod
+    def _check_packed_metadata(kv_cache, position_ids, slot_mapping, block_tables,
+                               query_start_loc, context_lens, max_query_len,
+                               num_tokens) -> None:
+        bs, width = kv_cache.block_size, block_tables.shape[1]
+        device = position_ids.device
+        lens = query_start_loc[1:] - query_start_loc[:-1]
+        owner = torch.repeat_interleave(
+            torch.arange(context_lens.shape[0], device=device), lens.clamp(min=0),
+            output_size=num_tokens)
+        first = (context_lens - lens)[owner]
+        offset = torch.arange(num_tokens, device=device) - query_start_loc[:-1][owner]
+        required = (context_lens + bs - 1) // bs
+        used = torch.arange(width, device=device)[None, :] < required[:, None]
+        col = (position_ids // bs).clamp(0, max(width - 1, 0))
+        expected = block_tables[owner, col] * bs + position_ids % bs
+        ordered = slot_mapping.sort().values
+        flags = torch.stack([
+            query_start_loc[0] != 0,
+            (lens <= 0).any(),
+            query_start_loc[-1] != num_tokens,
+            (lens > max_query_len).any(),
+            (context_lens < lens).any(),
+            (required > width).any(),
+            (used & ((block_tables < 0) | (block_tables >= kv_cache.num_blocks))).any(),
+            (position_ids != first + offset).any(),
+            (slot_mapping != expected).any(),
+            (ordered[1:] == ordered[:-1]).any(),
+        ]).tolist()
+        _raise_first([
+            (flags[0], ValueError("query_start_loc must start at 0")),
+            (flags[1], ValueError("query_start_loc must be strictly increasing")),
+            (flags[2], ValueError("query_start_loc must end at the packed token count")),
+            (flags[3], ValueError("max_query_len is smaller than a request's token count")),
+            (flags[4], ValueError("context_lens must cover each request's tokens")),
+            (flags[5], ValueError("block_tables have insufficient blocks for context_lens")),
+            (flags[6], ValueError("block_tables contain an invalid physical block")),
+            (flags[7], ValueError("position_ids must run from context_len - num_tokens "
+                                  "to context_len - 1 for each request")),
+            (flags[8], ValueError("slot_mapping must match block_tables and positions")),
+            (flags[9], ValueError("packed tokens must use distinct write slots")),
+        ])
+
+
+class TinyQwen2ForCausalLM(nn.Module):
+    """Backbone + lm_head (reference :1170-1240)."""
+
+    def __init__(self, config: TinyQwen2Config) -> None:
+        super().__init__()
+        self.model = TinyQwen2Model(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    def forward(self, input_ids, position_ids=None) -> torch.Tensor:
+        return self.lm_head(self.model(input_ids, position_ids))
+
+    def forward_prefill_with_cache(self, input_ids, position_ids, kv_cache,
+                                   slot_mapping) -> torch.Tensor:
+        return self.lm_head(self.model.forward_prefill_with_cache(
+            input_ids=input_ids, position_ids=position_ids, kv_cache=kv_cache,
+            slot_mapping=slot_mapping))
+
+    def forward_decode_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
+                                  block_table, context_len) -> torch.Tensor:
+        return self.lm_head(self.model.forward_decode_with_cache(
+            input_ids=input_ids, position_ids=position_ids, kv_cache=kv_cache,
+            slot_mapping=slot_mapping, block_table=block_table, context_len=context_len))
+
+    def forward_decode_batch_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
+                                        block_tables, context_lens) -> torch.Tensor:
+        """[B, 1] -> [B, 1, vocab_size] logits."""
+        return self.lm_head(self.model.forward_decode_batch_with_cache(
+            input_ids=input_ids, position_ids=position_ids, kv_cache=kv_cache,
+            slot_mapping=slot_mapping, block_tables=block_tables, context_lens=context_lens))
+
+    def forward_prefill_packed_with_cache(self, input_ids, position_ids, kv_cache,
+                                          slot_mapping, block_tables, query_start_loc,
+                                          context_lens, max_query_len) -> torch.Tensor:
+        """[T] -> [T, vocab_size] logits for the packed prefill tokens."""
+        return self.lm_head(self.model.forward_prefill_packed_with_cache(
+            input_ids, position_ids, kv_cache, slot_mapping, block_tables, query_start_loc,
+            context_lens, max_query_len))

@@ -355,6 +355,40 @@ class Qwen2Attention(nn.Module):
         ])
 
     # ------------------------------------------------------------------
+    # Packed prefill of several requests (no counterpart in the reference's
+    # attention; its runner calls forward_prefill_with_cache per request,
+    # runtime/model_runner.py:254-266)
+    # ------------------------------------------------------------------
+    def forward_prefill_packed_with_cache(self, hidden_states: torch.Tensor,
+                                          position_ids: torch.Tensor, kv_cache: PagedKVCache,
+                                          layer_idx: int, slot_mapping: torch.Tensor,
+                                          block_tables: torch.Tensor,
+                                          query_start_loc: torch.Tensor,
+                                          context_lens: torch.Tensor,
+                                          max_query_len: int) -> torch.Tensor:
+        """Prefill the packed tokens [T, hidden] of R requests: request r owns
+        rows query_start_loc[r]:query_start_loc[r+1], which sit at positions
+        context_lens[r] - len_r .. context_lens[r] - 1 and are written to
+        slot_mapping before attending causally over the request's cached
+        prefix and themselves (one mlr_kv_write, one mlr_paged_prefill).
+
+        The caller has validated the metadata (TinyQwen2Model does, once per
+        forward): positions follow the layout above, slots follow the block
+        tables and are distinct."""
+        if hidden_states.ndim != 2 or hidden_states.shape[1] != self.hidden_size:
+            raise ValueError("hidden_states must have shape [num_tokens, hidden_size]")
+        if position_ids.shape != hidden_states.shape[:1]:
+            raise ValueError("position_ids must have shape [num_tokens]")
+        query, key, value = self._qkv_rope(hidden_states.unsqueeze(0), position_ids.unsqueeze(0))
+        kv_cache.write_slots(slot_mapping=slot_mapping, k=key.squeeze(0), v=value.squeeze(0),
+                             layer_idx=layer_idx, validate=False)
+        k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)
+        out = kpa.paged_prefill_launch(query.squeeze(0).contiguous(), k_layer, v_layer,
+                                       block_tables, query_start_loc, context_lens,
+                                       max_query_len)
+        return self.o_proj(out.reshape(-1, self.hidden_size))
+
+    # ------------------------------------------------------------------
     # Chunk prefill (reference :624-767)
     # ------------------------------------------------------------------
     def forward_prefill_chunk_with_cache(self, hidden_states: torch.Tensor,

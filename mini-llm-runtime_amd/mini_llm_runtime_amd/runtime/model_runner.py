@@ -1,0 +1,299 @@
+"""One serving step: schedule -> pack -> forward -> sample -> update
+(reference runtime/model_runner.py:13-388).
+
+``build_model_batch`` packs the scheduled requests (prefills first, then
+decodes) into flat token/position arrays with ``query_start_loc`` offsets and
+the paged-attention metadata: right-padded (-1) block tables, context lengths
+and the slot of every scheduled token, slot = table[pos // B] * B + pos % B.
+
+``execute_model_batch`` runs the model on those metadata. The reference runs
+one ``forward_prefill_with_cache`` per prefill request; here every prefill of
+the step goes through one packed forward (``forward_prefill_packed_with_cache``:
+one varlen prefill launch per layer), and the decodes through one batched
+decode forward, as in the reference. Logits come back in packed token order
+whatever the order of phases in the batch. The batch checks are the
+reference's, with its messages and order, evaluated with two host syncs
+instead of several per request.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .paged_kv_cache import PagedKVCache
+from .request import Request, RequestStatus
+from .scheduler import Scheduler, SchedulerOutput
+
+
+@dataclass
+class ModelBatch:
+    """Flattened model inputs of all requests in one scheduler step."""
+
+    request_ids: list[str]
+    input_token_ids: torch.Tensor
+    positions: torch.Tensor
+    query_start_loc: torch.Tensor
+    request_phases: list[RequestStatus]
+    context_lens: torch.Tensor
+    block_tables: torch.Tensor
+    slot_mapping: torch.Tensor
+
+
+@dataclass
+class GenerationStepResult:
+    scheduler_output: SchedulerOutput
+    model_batch: ModelBatch
+    packed_logits: torch.Tensor
+    sampled_token_ids: dict[str, int]
+    finished_requests: list[Request]
+
+
+def _slots(request: Request, start: int, count: int, block_size: int) -> list[int]:
+    table = request.block_table
+    last = start + count - 1
+    if count > 0 and last // block_size >= len(table):
+        # The first position without a block, as the reference reports it.
+        missing = max(start, len(table) * block_size)
+        raise ValueError(f"Request {request.request_id} has no KV cache block "
+                         f"for position {missing}")
+    return [table[p // block_size] * block_size + p % block_size
+            for p in range(start, start + count)]
+
+
+def build_model_batch(scheduler_output: SchedulerOutput, block_size: int,
+                      device: torch.device | str = "cpu") -> ModelBatch:
+    if block_size <= 0:
+        raise ValueError("block_size must be greater than 0")
+    ids: list[str] = []
+    phases: list[RequestStatus] = []
+    tokens: list[int] = []
+    positions: list[int] = []
+    qsl = [0]
+    ctx: list[int] = []
+    tables: list[list[int]] = []
+    slots: list[int] = []
+
+    def add(request: Request, phase: RequestStatus, new_tokens: list[int], start: int):
+        count = len(new_tokens)
+        slots.extend(_slots(request, start, count, block_size))
+        ids.append(request.request_id)
+        phases.append(phase)
+        tokens.extend(new_tokens)
+        positions.extend(range(start, start + count))
+        qsl.append(qsl[-1] + count)
+        ctx.append(start + count)
+        tables.append(list(request.block_table))
+
+    for request in scheduler_output.prefill_requests:
+        count = scheduler_output.num_scheduled_tokens[request.request_id]
+        start = request.num_computed_tokens
+        chunk = request.prompt_token_ids[start:start + count]
+        if len(chunk) != count:
+            raise ValueError(f"Request {request.request_id} expected {count} prefill "
+                             f"tokens, got {len(chunk)}")
+        add(request, RequestStatus.PREFILLING, chunk, start)
+
+    for request in scheduler_output.decode_requests:
+        if scheduler_output.num_scheduled_tokens[request.request_id] != 1:
+            raise ValueError("Decode currently supports exactly one token per request")
+        pending = request.pending_token_id
+        if pending is None:
+            raise ValueError(f"Decode request {request.request_id} has no pending token")
+        add(request, RequestStatus.DECODING, [pending], request.num_computed_tokens)
+
+    dev = torch.device(device)
+    width = max((len(t) for t in tables), default=0)
+    padded = [t + [-1] * (width - len(t)) for t in tables]
+
+    def long(values) -> torch.Tensor:
+        return torch.tensor(values, dtype=torch.long, device=dev)
+
+    return ModelBatch(
+        request_ids=ids,
+        input_token_ids=long(tokens),
+        positions=long(positions),
+        query_start_loc=long(qsl),
+        request_phases=phases,
+        context_lens=long(ctx),
+        block_tables=long(padded) if tables else torch.empty((0, 0), dtype=torch.long,
+                                                              device=dev),
+        slot_mapping=long(slots),
+    )
+
+
+def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list[int], int]:
+    """The reference's execute_model_batch checks (:154-243), in its order.
+    Returns the host copy of query_start_loc and the packed token count."""
+    n = len(batch.request_ids)
+    if len(batch.request_phases) != n:
+        raise ValueError("request_phases length must match request_ids")
+    if not n:
+        raise ValueError("Cannot execute an empty ModelBatch")
+    for name in ("input_token_ids", "positions", "slot_mapping"):
+        if getattr(batch, name).ndim != 1:
+            raise ValueError(f"{name} must be one-dimensional")
+    num_tokens = batch.input_token_ids.numel()
+    if batch.positions.numel() != num_tokens:
+        raise ValueError("positions length must match input_token_ids")
+    if batch.slot_mapping.numel() != num_tokens:
+        raise ValueError("slot_mapping length must match input_token_ids")
+    if batch.context_lens.ndim != 1:
+        raise ValueError("context_lens must be one-dimensional")
+    if batch.context_lens.numel() != n:
+        raise ValueError("context_lens length must match request_ids")
+    if batch.block_tables.ndim != 2:
+        raise ValueError("block_tables must be two-dimensional")
+    if batch.block_tables.shape[0] != n:
+        raise ValueError("block_tables rows must match request_ids")
+    index = {"input_token_ids": batch.input_token_ids, "positions": batch.positions,
+             "query_start_loc": batch.query_start_loc, "context_lens": batch.context_lens,
+             "block_tables": batch.block_tables, "slot_mapping": batch.slot_mapping}
+    for name, tensor in index.items():
+        if tensor.dtype is not torch.long:
+            raise ValueError(f"{name} must use torch.long dtype")
+    device = batch.input_token_ids.device
+    for name, tensor in index.items():
+        if tensor.device != device:
+            raise ValueError(f"{name} must be on the same device as input_token_ids")
+    param = next(model.parameters())
+    if device != param.device:
+        raise ValueError("ModelBatch and model must be on the same device")
+    if kv_cache.device != param.device:
+        raise ValueError("KV cache and model must be on the same device")
+    if kv_cache.dtype != param.dtype:
+        raise ValueError("KV cache dtype must match model dtype")
+    if batch.query_start_loc.ndim != 1:
+        raise ValueError("query_start_loc must be one-dimensional")
+    if batch.query_start_loc.numel() != n + 1:
+        raise ValueError("query_start_loc must contain one more entry than request_ids")
+
+    # Everything the data-dependent checks need, in one transfer.
+    qsl = batch.query_start_loc.tolist()
+    ctx = batch.context_lens.tolist()
+    if qsl[0] != 0:
+        raise ValueError("query_start_loc must start at 0")
+    if any(b <= a for a, b in zip(qsl, qsl[1:])):
+        raise ValueError("query_start_loc must be strictly increasing")
+    if qsl[-1] != num_tokens:
+        raise ValueError("query_start_loc must end at the packed token count")
+    bs, width = kv_cache.block_size, batch.block_tables.shape[1]
+    required = [-(-c // bs) if c > 0 else 0 for c in ctx]
+    cols = torch.arange(width, device=device)
+    req_t = torch.tensor(required, dtype=torch.long, device=device)
+    used = cols[None, :] < req_t[:, None]
+    bad_rows = (used & ((batch.block_tables < 0)
+                        | (batch.block_tables >= kv_cache.num_blocks))).any(dim=1).tolist()
+    for i, request_id in enumerate(batch.request_ids):
+        if ctx[i] <= 0:
+            raise ValueError(f"Request {request_id} context_len must be greater than 0")
+        if width < required[i]:
+            raise ValueError(f"Request {request_id} block_table has insufficient blocks")
+        if bad_rows[i]:
+            raise ValueError(f"Request {request_id} block_table contains an invalid "
+                             "physical block")
+    for i, phase in enumerate(batch.request_phases):
+        if phase is RequestStatus.DECODING:
+            if qsl[i + 1] - qsl[i] != 1:
+                raise ValueError("Decode requires exactly one token per request")
+        elif phase is not RequestStatus.PREFILLING:
+            raise ValueError(f"Unsupported request phase {phase} for request "
+                             f"{batch.request_ids[i]}")
+    return qsl, num_tokens
+
+
+def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> torch.Tensor:
+    """[num_packed_tokens, vocab_size] logits in packed token order."""
+    qsl, num_tokens = _check_batch(model, batch, kv_cache)
+    device = batch.input_token_ids.device
+    logits = model.lm_head.weight.new_empty((num_tokens, model.lm_head.out_features))
+    prefill = [i for i, ph in enumerate(batch.request_phases) if ph is RequestStatus.PREFILLING]
+    decode = [i for i, ph in enumerate(batch.request_phases) if ph is RequestStatus.DECODING]
+
+    if prefill:
+        lens = [qsl[i + 1] - qsl[i] for i in prefill]
+        contiguous = prefill == list(range(len(prefill)))
+        if contiguous:  # build_model_batch's order: the prefill tokens lead
+            rows = slice(0, qsl[len(prefill)])
+            pick = lambda t: t[rows]  # noqa: E731
+        else:
+            idx = torch.cat([torch.arange(qsl[i], qsl[i + 1]) for i in prefill]).to(device)
+            pick = lambda t: t.index_select(0, idx)  # noqa: E731
+        req = torch.tensor(prefill, dtype=torch.long, device=device)
+        offsets = [0]
+        for n in lens:
+            offsets.append(offsets[-1] + n)
+        out = model.forward_prefill_packed_with_cache(
+            pick(batch.input_token_ids), pick(batch.positions), kv_cache,
+            pick(batch.slot_mapping), batch.block_tables.index_select(0, req),
+            torch.tensor(offsets, dtype=torch.long, device=device),
+            batch.context_lens.index_select(0, req), max(lens))
+        if contiguous:
+            logits[rows] = out
+        else:
+            logits.index_copy_(0, idx, out)
+
+    if decode:
+        req = torch.tensor(decode, dtype=torch.long, device=device)
+        rows = torch.tensor([qsl[i] for i in decode], dtype=torch.long, device=device)
+        out = model.forward_decode_batch_with_cache(
+            input_ids=batch.input_token_ids.index_select(0, rows).unsqueeze(1),
+            position_ids=batch.positions.index_select(0, rows).unsqueeze(1),
+            kv_cache=kv_cache,
+            slot_mapping=batch.slot_mapping.index_select(0, rows),
+            block_tables=batch.block_tables.index_select(0, req),
+            context_lens=batch.context_lens.index_select(0, req))
+        logits.index_copy_(0, rows, out.squeeze(1))
+    return logits
+
+
+def greedy_sample(packed_logits: torch.Tensor, batch: ModelBatch) -> dict[str, int]:
+    """Argmax of each request's last scheduled token (reference :287-322)."""
+    if packed_logits.ndim != 2:
+        raise ValueError("packed_logits must have shape [total_tokens, vocab_size]")
+    if packed_logits.shape[0] != batch.input_token_ids.shape[0]:
+        raise ValueError("packed_logits token dimension must match ModelBatch tokens")
+    if len(batch.request_ids) + 1 != batch.query_start_loc.numel():
+        raise ValueError("query_start_loc must contain one more entry than request_ids")
+    qsl = batch.query_start_loc.tolist()
+    for i, request_id in enumerate(batch.request_ids):
+        if qsl[i + 1] <= qsl[i]:
+            raise ValueError(f"Request {request_id} must contain at least one query token")
+    if not batch.request_ids:
+        return {}
+    last = torch.tensor([end - 1 for end in qsl[1:]], dtype=torch.long,
+                        device=packed_logits.device)
+    picks = packed_logits.index_select(0, last).argmax(dim=-1).tolist()
+    return dict(zip(batch.request_ids, (int(t) for t in picks)))
+
+
+def run_generation_step(model, scheduler: Scheduler,
+                        eos_token_id: int | None = None) -> GenerationStepResult:
+    if not scheduler.waiting and not scheduler.running:
+        raise ValueError("Cannot run generation step with no requests")
+    scheduler_output = scheduler.schedule()
+    if scheduler_output.is_empty:
+        raise RuntimeError("Scheduler made no progress while unfinished requests remain")
+    batch = build_model_batch(scheduler_output, block_size=scheduler.kv_cache.block_size,
+                              device=scheduler.kv_cache.device)
+    packed_logits = execute_model_batch(model=model, batch=batch, kv_cache=scheduler.kv_cache)
+    sampled = greedy_sample(packed_logits, batch)
+    eos = ({rid for rid, tok in sampled.items() if tok == eos_token_id}
+           if eos_token_id is not None else set())
+    finished = scheduler.update_after_model(scheduler_output=scheduler_output,
+                                            sampled_token_ids=sampled,
+                                            reached_eos_request_ids=eos)
+    return GenerationStepResult(scheduler_output=scheduler_output, model_batch=batch,
+                                packed_logits=packed_logits, sampled_token_ids=sampled,
+                                finished_requests=finished)
+
+
+def run_greedy_generation(model, scheduler: Scheduler,
+                          eos_token_id: int | None = None) -> list[Request]:
+    """Schedule-model-sample-update until every request has finished."""
+    finished: list[Request] = []
+    while scheduler.waiting or scheduler.running:
+        finished.extend(run_generation_step(model, scheduler,
+                                            eos_token_id=eos_token_id).finished_requests)
+    return finished

@@ -11,6 +11,7 @@ plants mistakes in copies of the oracle and requires every mistake to fail.
 from __future__ import annotations
 
 import os
+import types
 
 import numpy as np
 import torch
@@ -314,3 +315,94 @@ def check_qwen2_callers_vs_textbook(mod):
 
 
 QWEN2_CHECKS = (check_qwen2_callers_vs_textbook,)
+
+
+# ---------------------------------------------------------------------------
+# Whole model (oracle/qwen2_model.py) against a float64 textbook: RMSNorm as
+# x / sqrt(mean(x^2) + eps) * w (eps large enough to matter), SwiGLU with
+# silu(x) = x / (1 + e^-x), pre-norm residual layers, the attention of the
+# callers' textbook above, final norm and lm_head.
+# ---------------------------------------------------------------------------
+MODEL_CFG = types.SimpleNamespace(
+    vocab_size=23, hidden_size=32, intermediate_size=40, num_hidden_layers=2,
+    num_attention_heads=4, num_key_value_heads=2, head_dim=8, rope_theta=10000.0,
+    rms_norm_eps=0.25)
+
+
+def model_state(seed=0):
+    cfg = MODEL_CFG
+    gen = torch.Generator().manual_seed(seed)
+    rnd = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64) * 0.4  # noqa: E731
+    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    hid, inter = cfg.hidden_size, cfg.intermediate_size
+    sd = {"model.embed_tokens.weight": rnd(cfg.vocab_size, hid),
+          "model.norm.weight": 1 + rnd(hid), "lm_head.weight": rnd(cfg.vocab_size, hid)}
+    for i in range(cfg.num_hidden_layers):
+        p = f"model.layers.{i}."
+        a = p + "self_attn."
+        sd.update({p + "input_layernorm.weight": 1 + rnd(hid),
+                   p + "post_attention_layernorm.weight": 1 + rnd(hid),
+                   a + "qkv_proj.q_proj.weight": rnd(hq * d, hid), a + "qkv_proj.q_proj.bias": rnd(hq * d),
+                   a + "qkv_proj.k_proj.weight": rnd(hkv * d, hid), a + "qkv_proj.k_proj.bias": rnd(hkv * d),
+                   a + "qkv_proj.v_proj.weight": rnd(hkv * d, hid), a + "qkv_proj.v_proj.bias": rnd(hkv * d),
+                   a + "o_proj.weight": rnd(hid, hid),
+                   p + "mlp.gate_proj.weight": rnd(inter, hid),
+                   p + "mlp.up_proj.weight": rnd(inter, hid),
+                   p + "mlp.down_proj.weight": rnd(hid, inter)})
+    return sd
+
+
+def _np_rms(x, w, eps):
+    return x / np.sqrt(np.mean(x * x) + eps) * w
+
+
+def np_model_logits(sd, tokens):
+    """Logits [S, vocab] of the sequence, position by position."""
+    cfg = MODEL_CFG
+    n = {k: v.numpy() for k, v in sd.items()}
+    hs = [n["model.embed_tokens.weight"][t].copy() for t in tokens]
+    for i in range(cfg.num_hidden_layers):
+        p = f"model.layers.{i}."
+        a = p + "self_attn.qkv_proj."
+        w = {"q_w": sd[a + "q_proj.weight"], "q_b": sd[a + "q_proj.bias"],
+             "k_w": sd[a + "k_proj.weight"], "k_b": sd[a + "k_proj.bias"],
+             "v_w": sd[a + "v_proj.weight"], "v_b": sd[a + "v_proj.bias"]}
+        qkv = [_np_qkv(_np_rms(h, n[p + "input_layernorm.weight"], cfg.rms_norm_eps), w, t)
+               for t, h in enumerate(hs)]
+        keys = np.stack([x[1] for x in qkv])
+        vals = np.stack([x[2] for x in qkv])
+        wo = n[p + "self_attn.o_proj.weight"]
+        hs = [h + wo @ _np_attend(qkv[t][0], keys, vals, t + 1) for t, h in enumerate(hs)]
+        out = []
+        for h in hs:
+            x = _np_rms(h, n[p + "post_attention_layernorm.weight"], cfg.rms_norm_eps)
+            g = n[p + "mlp.gate_proj.weight"] @ x
+            u = n[p + "mlp.up_proj.weight"] @ x
+            out.append(h + n[p + "mlp.down_proj.weight"] @ (g / (1 + np.exp(-g)) * u))
+        hs = out
+    return np.stack([n["lm_head.weight"] @ _np_rms(h, n["model.norm.weight"], cfg.rms_norm_eps)
+                     for h in hs])
+
+
+def check_model_vs_textbook(mod):
+    # Tolerance 1e-6: FP32 RoPE tables, as in the callers' check above.
+    sd = model_state()
+    oracle = mod.OracleQwen2(sd, MODEL_CFG)
+    gen = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, MODEL_CFG.vocab_size, (9,), generator=gen).tolist()
+    np.testing.assert_allclose(oracle.forward(prompt).numpy(), np_model_logits(sd, prompt),
+                               rtol=1e-6, atol=1e-6)
+    # Greedy decoding, both ways, against the textbook's argmax and margins.
+    margins: list = []
+    cached = oracle.cached_greedy(prompt, 6, margins)
+    assert oracle.dense_greedy(prompt, 6) == cached
+    seq = list(prompt)
+    for step in range(6):
+        row = np_model_logits(sd, seq)[-1]
+        order = np.argsort(row)[::-1]
+        assert cached[step] == int(order[0])
+        assert abs(margins[step][0] - (row[order[0]] - row[order[1]])) < 1e-6
+        seq.append(cached[step])
+
+
+MODEL_CHECKS = (check_model_vs_textbook,)

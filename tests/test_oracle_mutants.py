@@ -115,3 +115,42 @@ def test_qwen2_pins_catch_planted_mistake(name):
         except (AssertionError, IndexError, RuntimeError, ValueError):
             caught.append(check.__name__)
     assert caught, f"no pin detects the planted mistake {name!r}"
+
+
+# And for the whole model (oracle/qwen2_model.py).
+MODEL_MUTATIONS = {
+    "rmsnorm-eps-dropped": (
+        "normalized = h * torch.rsqrt(h.square().mean(dim=-1, keepdim=True) + eps)",
+        "normalized = h * torch.rsqrt(h.square().mean(dim=-1, keepdim=True))",
+    ),
+    "mlp-gate-up-swapped": (
+        "return F.linear(F.silu(F.linear(x, gate_w)) * F.linear(x, up_w), down_w)",
+        "return F.linear(F.silu(F.linear(x, up_w)) * F.linear(x, gate_w), down_w)",
+    ),
+    "final-norm-skipped": (
+        "return F.linear(rms_norm(h, self.norm_w, self.cfg.rms_norm_eps), self.lm_head)",
+        "return F.linear(h, self.lm_head)",
+    ),
+    "cached-decode-position-off-by-one": (
+        "p = len(prompt) + len(out) - 1",
+        "p = len(prompt) + len(out)",
+    ),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MODEL_MUTATIONS))
+def test_model_pins_catch_planted_mistake(name):
+    import oracle.qwen2_model as qm
+    before, after = MODEL_MUTATIONS[name]
+    source = inspect.getsource(qm)
+    assert source.count(before) == 1, f"mutation site for {name} not found exactly once"
+    module = types.ModuleType(f"oracle.model_mutant_{name.replace('-', '_')}")
+    module.__package__ = "oracle"
+    exec(compile(source.replace(before, after), module.__name__, "exec"), module.__dict__)
+    caught = []
+    for check in oracle_pins.MODEL_CHECKS:
+        try:
+            check(module)
+        except (AssertionError, IndexError, RuntimeError, ValueError):
+            caught.append(check.__name__)
+    assert caught, f"no pin detects the planted mistake {name!r}"

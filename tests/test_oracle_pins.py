@@ -98,3 +98,9 @@ def test_slot_formula_and_padding():
     with pytest.raises(ValueError, match="no KV cache block"):
         slots_for_positions(table, [12], 4)
     assert pad_block_tables([[1], [2, 3, 4], []]) == [[1, -1, -1], [2, 3, 4], [-1, -1, -1]]
+
+
+@pytest.mark.parametrize("check", oracle_pins.MODEL_CHECKS, ids=lambda c: c.__name__)
+def test_oracle_model_is_pinned(check):
+    import oracle.qwen2_model as qm
+    check(qm)
