@@ -24,6 +24,11 @@ same inputs with all host cores.
 A secondary object reports BF16 chunk prefill (8 x 512-token chunks on
 prefixes U[0, 3584]) in TFLOP/s against the 2.5 PFLOP/s bf16 MFMA peak.
 
+A third, ``serving``, times end-to-end continuous-batching steps of a
+random-init Qwen2.5-0.5B-shape model in BF16 (workloads.qwen05b_serving:
+about 48 decodes + 2 x 1024-token prefills per step, 128 steps after the
+warm-up): ms per step and tokens per second.
+
     python bench.py [--gpus 1] [--steps 240] [--warmup 48]
 
 ``--profile`` launches the same kernels eagerly and untimed, for rocprofv3:
@@ -65,6 +70,10 @@ def parse_args():
     p.add_argument("--tokens-per-split", type=int, default=0)
     p.add_argument("--profile", action="store_true",
                    help="launch the kernels eagerly, untimed (for rocprofv3)")
+    p.add_argument("--serving", action="store_true",
+                   help="time only the end-to-end serving steps (qwen05b_serving, BF16)")
+    p.add_argument("--no-serving", action="store_true",
+                   help="leave the serving steps out of the default run")
     return p.parse_args()
 
 
@@ -329,6 +338,49 @@ def cpu_baseline_prefill(wl, budget):
     }
 
 
+def bench_serving(device, steps=None):
+    """End-to-end continuous-batching steps at Qwen2.5-0.5B shape in BF16
+    (workloads.qwen05b_serving): schedule, pack, 24-layer forward on the HIP
+    attention kernels with PyTorch GEMMs, sample, update. After the warm-up
+    (all 48 initial prompts admitted), each step is timed on the host with a
+    device synchronisation on both sides."""
+    import torch
+
+    from mini_llm_runtime_amd import workloads
+    from mini_llm_runtime_amd.runtime.model_runner import run_generation_step
+
+    w = workloads.qwen05b_serving()
+    steps = steps or w.steps
+    _, model, _, scheduler, _ = workloads.build_serving(w, device, torch.bfloat16)
+    times, decode_tokens, prefill_tokens, finished = [], 0, 0, 0
+    with torch.no_grad():
+        warm = workloads.serving_warm_up(model, scheduler, len(w.initial))
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            result = run_generation_step(model, scheduler)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            out = result.scheduler_output
+            decode_tokens += len(out.decode_requests)
+            prefill_tokens += sum(out.num_scheduled_tokens[r.request_id]
+                                  for r in out.prefill_requests)
+            finished += len(result.finished_requests)
+    total = sum(times)
+    return {
+        "workload": w.name,
+        "warmup_steps": warm,
+        "steps": steps,
+        "ms_per_step": round(1e3 * total / steps, 3),
+        "ms_per_step_median": round(1e3 * statistics.median(times), 3),
+        "decode_tokens_per_step": round(decode_tokens / steps, 2),
+        "prefill_tokens_per_step": round(prefill_tokens / steps, 2),
+        "tokens_per_s": round((decode_tokens + prefill_tokens) / total, 1),
+        "decode_tokens_per_s": round(decode_tokens / total, 1),
+        "requests_finished": finished,
+    }
+
+
 def measured_traffic():
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (profiles/traffic.json), or None when it is absent."""
@@ -352,6 +404,10 @@ def main():
     device = torch.device("cuda", 0)
     if args.profile:
         profile_run(args, device)
+        return
+    if args.serving:
+        print(json.dumps({"metric": "serving step (qwen05b_serving, bf16)",
+                          **bench_serving(device)}), flush=True)
         return
     dec = bench_decode(args, device)
     pre = None if args.no_prefill else bench_prefill(device)
@@ -414,6 +470,8 @@ def main():
             "us_per_call_by_kv_tile": pre["us_per_call"],
             "cpu_baseline": cpu_pre,
         }
+    if not args.no_serving:
+        line["serving"] = bench_serving(device)
     print(json.dumps(line), flush=True)
 
 

@@ -179,3 +179,100 @@ def bf16_prefill_chunk512_x8(num_seqs: int = 8, chunk: int = 512, max_prefix: in
     return PrefillWorkload("bf16_prefill_chunk512_x8", torch.cat(qs), torch.cat(cks),
                            torch.cat(cvs), k_cache, v_cache, bt, qsl, ctx, torch.cat(slots),
                            prefix, tables, bs)
+
+
+# ---------------------------------------------------------------------------
+# End-to-end continuous batching at Qwen2.5-0.5B shape
+# ---------------------------------------------------------------------------
+QWEN05B_CONFIG = dict(vocab_size=151936, hidden_size=896, intermediate_size=4864,
+                      num_hidden_layers=24, num_attention_heads=14, num_key_value_heads=2,
+                      max_position_embeddings=32768, rope_theta=1_000_000.0,
+                      rms_norm_eps=1e-6, tie_word_embeddings=False)
+
+
+@dataclass
+class ServingWorkload:
+    """A random-init model, the requests of a serving run and its scheduler
+    limits. ``initial`` requests (prompt, max_new_tokens) arrive first,
+    ``arrivals`` queue behind them; once every initial prompt is admitted
+    (the warm-up), ``steps`` scheduler steps are the measured run."""
+
+    name: str
+    config: dict
+    model_seed: int
+    block_size: int
+    num_blocks: int
+    max_num_batched_tokens: int
+    max_num_seqs: int
+    initial: list = field(default_factory=list)
+    arrivals: list = field(default_factory=list)
+    steps: int = 128
+
+
+def qwen05b_serving(num_initial: int = 48, prefills_per_step: int = 2,
+                    prefill_len: int = 1024, num_arrivals: int = 320,
+                    steps: int = 128) -> ServingWorkload:
+    """Mixed serving steps at Qwen2.5-0.5B shape (24 layers, hidden 896,
+    intermediate 4864, 14 / 2 heads, head_dim 64, vocab 151936, RoPE theta 1e6;
+    the lm_head is its own matrix so that a random model's tokens depend on
+    the context). 48 requests with prompts U[64, 2048] decode while prompts of
+    1024 random token ids arrive; the scheduler's budget (48 decode tokens +
+    2 x 1024) and 50 seats give about 48 decodes and 2 prefills per step.
+    Lifetimes of U[1, 49] and U[10, 40] new tokens (25 on average) retire
+    about two requests per step, so admission, exit and block reuse go on for
+    the whole run."""
+    gen = torch.Generator().manual_seed(0)
+    vocab = QWEN05B_CONFIG["vocab_size"]
+
+    def prompt(n):
+        return torch.randint(0, vocab, (n,), generator=gen).tolist()
+
+    initial = [(prompt(int(n)), int(m)) for n, m in zip(
+        torch.randint(64, 2049, (num_initial,), generator=gen),
+        torch.randint(1, 50, (num_initial,), generator=gen))]
+    arrivals = [(prompt(prefill_len), int(m))
+                for m in torch.randint(10, 41, (num_arrivals,), generator=gen)]
+    budget = num_initial + prefills_per_step * prefill_len
+    # Pool: every seat at its longest context (2048 + 49 tokens), plus slack.
+    block_size = 16
+    num_blocks = (num_initial + prefills_per_step) * math.ceil((2048 + 64) / block_size) + 256
+    return ServingWorkload(name="qwen05b_serving_48dec_2x1024pre", config=dict(QWEN05B_CONFIG),
+                           model_seed=0, block_size=block_size, num_blocks=num_blocks,
+                           max_num_batched_tokens=budget,
+                           max_num_seqs=num_initial + prefills_per_step,
+                           initial=initial, arrivals=arrivals, steps=steps)
+
+
+def build_serving(w: ServingWorkload, device, dtype):
+    """The model (seeded init on the CPU, then moved), its KV pool and a
+    scheduler holding every request of ``w`` (initial ones first)."""
+    from .model.qwen2 import TinyQwen2Config, TinyQwen2ForCausalLM
+    from .runtime.paged_kv_cache import PagedKVCache
+    from .runtime.request import Request
+    from .runtime.scheduler import Scheduler
+
+    cfg = TinyQwen2Config(**w.config)
+    torch.manual_seed(w.model_seed)
+    model = TinyQwen2ForCausalLM(cfg).to(device=device, dtype=dtype).eval()
+    cache = PagedKVCache(cfg.num_hidden_layers, w.num_blocks, w.block_size,
+                         cfg.num_key_value_heads, cfg.head_dim, dtype=dtype, device=device)
+    scheduler = Scheduler(w.max_num_batched_tokens, w.max_num_seqs, kv_cache=cache)
+    requests = [Request(f"init{i}", p, m, 0.0) for i, (p, m) in enumerate(w.initial)]
+    requests += [Request(f"arr{i}", p, m, 1.0 + i) for i, (p, m) in enumerate(w.arrivals)]
+    for request in requests:
+        scheduler.add_request(request)
+    return cfg, model, cache, scheduler, requests
+
+
+def serving_warm_up(model, scheduler, num_initial: int, max_steps: int = 1000) -> int:
+    """Run steps until every initial request has been admitted; returns the
+    number of steps run."""
+    from .runtime.model_runner import run_generation_step
+
+    steps = 0
+    while any(r.request_id.startswith("init") for r in scheduler.waiting):
+        run_generation_step(model, scheduler)
+        steps += 1
+        if steps > max_steps:
+            raise RuntimeError("warm-up did not admit the initial requests")
+    return steps

@@ -53,16 +53,16 @@ def make_model(cfg_kwargs, dtype, device, seed=0):
     return cfg, model.to(device=device, dtype=dtype).eval(), oracle
 
 
-def check_tokens(request, want, margins):
-    """request.output_token_ids == want, up to a near-tie step (see module)."""
-    got = request.output_token_ids
-    assert len(got) == len(want), (request.request_id, got, want)
+def check_tokens(request_id, got, want, margins):
+    """got == want, up to a near-tie step (see module). Returns the step of a
+    near-tie divergence, or None."""
+    assert len(got) == len(want), (request_id, got, want)
     for i, (g, w) in enumerate(zip(got, want)):
         if g == w:
             continue
         margin, second = margins[i]
         assert margin < NEAR_TIE and g == second, (
-            f"request {request.request_id} step {i}: got {g}, oracle {w} "
+            f"request {request_id} step {i}: got {g}, oracle {w} "
             f"(margin {margin:.3g}, second {second})")
         return i  # diverged at a near tie: the rest follows another context
     return None
@@ -105,7 +105,7 @@ def test_fp32_continuous_batching_matches_oracle(device, cfg_kwargs):
     for request in requests:
         margins: list = []
         want = oracle.cached_greedy(request.prompt_token_ids, request.max_new_tokens, margins)
-        check_tokens(request, want, margins)
+        check_tokens(request.request_id, request.output_token_ids, want, margins)
         assert request.status is RequestStatus.FINISHED
 
 
@@ -208,3 +208,38 @@ def test_bf16_qwen05b_shape_step_runs_and_tracks_oracle(device):
         want = oracle.cached_greedy(r.prompt_token_ids, 1, margins)
         if margins[0][0] > 0.5:
             assert r.output_token_ids[0] == want[0], (r.request_id, margins[0])
+
+
+def test_qwen05b_serving_fp32_matches_oracle_tokens(device):
+    """The Qwen2.5-0.5B-shape serving workload (24 layers; 48 decoding
+    requests with prompts U[64, 2048], 1024-token prompts arriving, about 48
+    decodes + 2 prefills per step) in FP32: the warm-up, then 128 steps. The
+    sampled requests' tokens equal the oracle's greedy tokens
+    (tests/golden/serving_qwen05b_fp32_tokens.json, from
+    tests/golden/make_serving_fp32_tokens.py), up to the near-tie rule."""
+    import json
+    import os
+
+    from conftest import GOLDEN
+    from mini_llm_runtime_amd import workloads
+
+    with open(os.path.join(GOLDEN, "serving_qwen05b_fp32_tokens.json")) as f:
+        golden = json.load(f)
+    w = workloads.qwen05b_serving()
+    _, model, cache, scheduler, requests = workloads.build_serving(w, device, torch.float32)
+    with torch.no_grad():
+        workloads.serving_warm_up(model, scheduler, len(w.initial))
+        for _ in range(w.steps):
+            run_generation_step(model, scheduler)
+    by_id = {r.request_id: r for r in requests}
+    compared = 0
+    for g in golden["requests"]:
+        r = by_id[g["request_id"]]
+        assert r.prompt_len == g["prompt_len"]
+        got = r.output_token_ids
+        assert got, f"{r.request_id} never ran"
+        margins = list(zip(g["margins"], g["second"]))
+        want = g["tokens"][:len(got)]
+        stopped = check_tokens(r.request_id, got, want, margins)
+        compared += len(got) if stopped is None else stopped
+    assert compared >= 200

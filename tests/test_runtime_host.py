@@ -268,3 +268,36 @@ def test_greedy_sample_uses_each_requests_last_token():
         greedy_sample(torch.zeros(2, 5), batch)
     with pytest.raises(ValueError, match=r"\[total_tokens, vocab_size\]"):
         greedy_sample(torch.zeros(3), batch)
+
+
+# ----------------------------------------------------------------------------
+# Block tables of the Qwen2.5-0.5B-shape serving run (workloads.qwen05b_serving)
+# against the oracle allocator (oracle/paged_kv_cache.py, the reference's LIFO
+# free list). The schedule does not depend on token values (no EOS), so a
+# bookkeeping-only run with dummy samples visits the same states.
+# ----------------------------------------------------------------------------
+def test_serving_schedule_block_tables_match_oracle_allocator():
+    from mini_llm_runtime_amd import workloads
+    from oracle.paged_kv_cache import OracleKVCache
+
+    w = workloads.qwen05b_serving()
+    runs = []
+    for cache in (PagedKVCache(1, w.num_blocks, w.block_size, 1, 1, dtype=torch.float32),
+                  OracleKVCache(1, w.num_blocks, w.block_size, 1, 1, dtype=torch.float32)):
+        s = Scheduler(w.max_num_batched_tokens, w.max_num_seqs, kv_cache=cache)
+        reqs = [Request(f"init{i}", p, m, 0.0) for i, (p, m) in enumerate(w.initial)]
+        reqs += [Request(f"arr{i}", p, m, 1.0) for i, (p, m) in enumerate(w.arrivals)]
+        for r in reqs:
+            s.add_request(r)
+        trace = []
+        for _ in range(160):
+            out = s.schedule()
+            batch = build_model_batch(out, w.block_size)
+            trace.append((batch.request_ids, batch.block_tables.tolist(),
+                          batch.slot_mapping.tolist()))
+            s.update_after_model(out, {r.request_id: 0 for r in out.scheduled_requests})
+        runs.append(trace)
+    assert runs[0] == runs[1]
+    # The run exercised admission, exit and reuse.
+    steps_with_prefill = sum(any(rid.startswith("arr") for rid in ids[:2]) for ids, _, _ in runs[0])
+    assert steps_with_prefill > 50
