@@ -412,29 +412,36 @@ __global__ __launch_bounds__(64) void decode_combine_mfma(DecodeParams p) {
   constexpr int C = D / 64;
   const int h = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
+  const float *ws_acc = static_cast<const float *>(p.ws_acc);
+  const int64_t row0 = ((int64_t)b * p.hq + h) * p.max_splits;
+  // Loads of chunk s0: rows past the last split repeat it (in bounds; their
+  // weight is zero). Unconditional, so that they issue back to back.
+  float a[kChunk][C];
+  float2 ml_raw;
+  auto load_chunk = [&](int s0, int last) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const int64_t row = row0 + min(s0 + j, last);
+#pragma unroll
+      for (int c = 0; c < C; ++c) a[j][c] = ws_acc[row * D + 64 * c + lane];
+    }
+    ml_raw = p.ws_ml[row0 + min(s0 + lane, last)];
+  };
+  // The first chunk goes out with the context length: one round trip for a
+  // sequence of at most kChunk splits.
+  load_chunk(0, p.max_splits - 1);
   const int64_t cap = p.max_blocks * p.block_size;
   int64_t ctx = p.ctx[b];
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int ns = static_cast<int>(ceil_div(ctx, p.ts));
   if (ns <= 1) return;
-  const float *ws_acc = static_cast<const float *>(p.ws_acc);
-  const int64_t row0 = ((int64_t)b * p.hq + h) * p.max_splits;
   float num[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) num[c] = 0.f;
   float den = 0.f, M = -INFINITY;
   for (int s0 = 0; s0 < ns; s0 += kChunk) {
+    if (s0 > 0) load_chunk(s0, ns - 1);
     const int cnt = min(kChunk, ns - s0);
-    // Unconditional loads (splits past cnt repeat the last one, weight 0): a
-    // load under a per-split branch would wait for the one before it.
-    float a[kChunk][C];
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      const int jc = j < cnt ? j : cnt - 1;
-#pragma unroll
-      for (int c = 0; c < C; ++c) a[j][c] = ws_acc[(row0 + s0 + jc) * D + 64 * c + lane];
-    }
-    const float2 ml_raw = p.ws_ml[row0 + s0 + (lane < cnt ? lane : 0)];
     const float2 ml = lane < cnt ? ml_raw : make_float2(-INFINITY, 0.f);
     const float m_new = fmaxf(M, wave_max(ml.x));
     const float rescale = __builtin_amdgcn_exp2f(M - m_new);  // 0 on the first chunk
@@ -446,8 +453,9 @@ __global__ __launch_bounds__(64) void decode_combine_mfma(DecodeParams p) {
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
       const float fj = __shfl(f, j);
+      // A select, not a product: rows past cnt may hold anything.
 #pragma unroll
-      for (int c = 0; c < C; ++c) num[c] += fj * a[j][c];
+      for (int c = 0; c < C; ++c) num[c] += j < cnt ? fj * a[j][c] : 0.f;
     }
   }
   uint16_t *out = static_cast<uint16_t *>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
