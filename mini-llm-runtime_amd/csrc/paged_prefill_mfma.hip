@@ -22,8 +22,11 @@
 //       B = Q^T fragments held in registers throughout.
 //   Lane l owns query l%32 and keys 8(i/4) + 4(l/32) + i%4 (i < 16) of each
 //   32-key block; lanes l and l^32 share a query, so the row max is one
-//   permlane32 swap. Base-2 online softmax in FP32; the reference point moves
-//   only when a tile raises the row max by more than kLazy (base-2 units), so
+//   permlane32 swap. Base-2 online softmax in FP32 with no per-score scaling:
+//   Q is pre-multiplied by scale*log2(e) and the S^T accumulator is seeded
+//   with -m, so the matrix cores return scores in base-2 units relative to the
+//   running reference point m and P = exp2(S^T) directly. The reference point
+//   moves only when a tile raises the row max by more than kLazy, so
 //   probabilities stay below 2^kLazy and numerator and denominator share it.
 //   O^T[32 dims x 32 queries] += V^T[32 dims x 16 keys] . P^T[16 keys x 32 q]
 //       B = P^T packed to bf16 straight from the S^T registers (k slot
@@ -36,10 +39,11 @@
 //
 // Numerics follow paged_attention_prefill_chunk_tiled
 // (kernels/reference/paged_attention.py:346-434): FP32 softmax statistics,
-// FP32 accumulation of P@V and one rounding of the output. Two roundings
+// FP32 accumulation of P@V and one rounding of the output. Three roundings
 // differ from the reference and stay far inside the 2e-2 tolerance of its
-// bf16 tests: P is rounded to bf16 as the MFMA operand, and q.k is not
-// rounded to bf16 before scaling (the reference rounds at :411-413).
+// bf16 tests: q*scale*log2(e) is rounded to bf16 (relative 2^-9 per element,
+// the size of the reference's own bf16 rounding of q.k at :411-413, which is
+// not done here), and P is rounded to bf16 as the MFMA operand.
 #include "paged_prefill.h"
 
 namespace mlr {
@@ -199,12 +203,20 @@ void prefill_mfma(PrefillParams p) {
   const int qpos = prefix + qi;
   const uint16_t *qrow = static_cast<const uint16_t *>(p.q) +
                          (rg.q0 + (q_ok ? qi : 0)) * p.q_st + static_cast<int64_t>(h) * p.q_sh;
+  // Pre-multiplied by scale*log2(e): the scores come out in base-2 units.
+  const float c2 = static_cast<float>(p.scale) * kLog2e;
   bf16x8_t qf[QS];
 #pragma unroll
   for (int s = 0; s < QS; ++s) {
     const uint4 raw = q_ok ? *reinterpret_cast<const uint4 *>(qrow + 16 * s + 8 * hh)
                            : make_uint4(0, 0, 0, 0);
-    qf[s] = __builtin_bit_cast(bf16x8_t, raw);
+    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+    uint32_t o4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o4[e] = bf16_pack2(__uint_as_float(w4[e] << 16) * c2,
+                         __uint_as_float(w4[e] & 0xffff0000u) * c2);
+    qf[s] = __builtin_bit_cast(bf16x8_t, make_uint4(o4[0], o4[1], o4[2], o4[3]));
   }
 
   // Copy role: copy i of a span moves chunk positions [64i, 64i + 64) of its 16
@@ -290,12 +302,16 @@ void prefill_mfma(PrefillParams p) {
       voff[half][n] = row * C::kRowB + ((((byte >> 4) ^ swz<D>(row)) << 4) | (byte & 15));
     }
 
-  const float c2 = static_cast<float>(p.scale) * kLog2e;  // score -> base 2
-  // Reference point of the running softmax (base 2). It starts at a finite
-  // floor, not -inf: a query can see no key at all in one split's tiles, and
-  // exp2(-inf - (-inf)) would be NaN. Masked scores stay -inf, so their
-  // probabilities are exactly 0 under any reference point.
-  float m_run = kFloor, l_run = 0.f;
+  // Reference point m of the running softmax (base 2). It stays at the
+  // finite floor kFloor (never -inf: a query can see no key at all in one
+  // split's tiles, and exp2(-inf - (-inf)) would be NaN) until the row sees a
+  // key. negm seeds S^T: -m, or 0 while m is unset. A tile needs the rescale
+  // when its relative max exceeds thr: kLazy once m is set, any visible key
+  // before. Masked scores stay -inf, so their probabilities are exactly 0.
+  float m_run = kFloor, l_run = 0.f, thr = -__FLT_MAX__;
+  f32x16_t negm;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) negm[i] = 0.f;
   f32x16_t acc[NB];
 #pragma unroll
   for (int n = 0; n < NB; ++n)
@@ -307,12 +323,10 @@ void prefill_mfma(PrefillParams p) {
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[j][i] = 0.f;
-#pragma unroll
       for (int st = 0; st < QS; ++st) {
         const bf16x8_t a =
             *reinterpret_cast<const bf16x8_t *>(kst + 32 * j * C::kRowB + koff[st]);
-        s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[st], s[j], 0, 0, 0);
+        s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[st], st == 0 ? negm : s[j], 0, 0, 0);
       }
     }
   };
@@ -328,7 +342,7 @@ void prefill_mfma(PrefillParams p) {
         if (dead) s[j][i] = -INFINITY;
       }
   };
-  // Row max of a tile in base-2 units: chains of eight, then the lane pair.
+  // Row max of a tile relative to m (base 2): chains of eight, then the lane pair.
   auto tile_max = [&](const f32x16_t (&s)[KB]) __attribute__((always_inline)) -> float {
     float mc[2 * KB];
 #pragma unroll
@@ -343,22 +357,33 @@ void prefill_mfma(PrefillParams p) {
     for (int width = KB; width >= 1; width >>= 1)
 #pragma unroll
       for (int c = 0; c < width; ++c) mc[c] = __builtin_elementwise_maximum(mc[c], mc[c + width]);
-    return pair_max(mc[0]) * c2;
+    return pair_max(mc[0]);
   };
-  // Moves the reference point when the tile max exceeds it by more than kLazy.
-  auto rescale = [&](float m_tile) __attribute__((always_inline)) {
-    const bool move = m_tile > m_run + kLazy;
-    if (__any(move)) {
-      const float m_new = move ? m_tile : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 1 where kept
+  // Moves the reference point to the tile max where that passed thr, rescales
+  // the accumulators and shifts the tile's scores to the new point.
+  auto rescale = [&](float m_rel, f32x16_t (&s)[KB]) __attribute__((always_inline)) {
+    if (__any(m_rel > thr)) {
+      const bool unset = m_run == kFloor;
+      const bool move = m_rel > thr;
+      const float m_new = move ? (unset ? 0.f : m_run) + m_rel : m_run;
+      const float shift = move ? m_rel : 0.f;
+      const float alpha = unset ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);  // 1 where kept
       l_run *= alpha;
 #pragma unroll
       for (int n = 0; n < NB; ++n) acc[n] *= alpha;
       m_run = m_new;
+      thr = m_new == kFloor ? -__FLT_MAX__ : kLazy;
+      const float seed = m_new == kFloor ? 0.f : -m_new;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) negm[i] = seed;
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[j][i] -= shift;
     }
   };
-  // P = exp2(S*c2 - m) packed to bf16, FP32 row sums (four chains; FP32 adds
-  // issue alongside the MFMAs, v_dot2 would not), and O^T += V^T P^T.
+  // P = exp2(S^T) packed to bf16, FP32 row sums (four chains; FP32 adds issue
+  // alongside the MFMAs, v_dot2 would not), and O^T += V^T P^T.
   auto attend = [&](const f32x16_t (&s)[KB], const unsigned char *vst) __attribute__((always_inline)) {
     float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -366,8 +391,8 @@ void prefill_mfma(PrefillParams p) {
       uint32_t pk[8];
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][2 * x], c2, -m_run));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][2 * x + 1], c2, -m_run));
+        const float p0 = __builtin_amdgcn_exp2f(s[j][2 * x]);
+        const float p1 = __builtin_amdgcn_exp2f(s[j][2 * x + 1]);
         pk[x] = bf16_pack2(p0, p1);
         lsum[(2 * x) & 3] += p0;
         lsum[(2 * x + 1) & 3] += p1;
@@ -417,7 +442,7 @@ void prefill_mfma(PrefillParams p) {
       scores(kEven ? ks0[split] : ks1[split], s);
       const uint64_t badw = read_bad(kEven ? badk0[split] : badk1[split]);
       if (t >= wave_nfull || badw != 0) mask(t, badw, s);
-      rescale(tile_max(s));
+      rescale(tile_max(s), s);
       attend(s, kEven ? vs0[split] : vs1[split]);
     }
     __syncthreads();
