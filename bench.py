@@ -67,6 +67,8 @@ def parse_args():
                    help="seconds of CPU-baseline work (bounded sample)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-pre-attention", action="store_true",
+                   help="skip the fused pre-attention (bias + RoPE + KV write) timing")
     p.add_argument("--tokens-per-split", type=int, default=0)
     p.add_argument("--profile", action="store_true",
                    help="launch the kernels eagerly, untimed (for rocprofv3)")
@@ -137,6 +139,28 @@ def profile_run(args, device):
                                          out=pout)
         torch.cuda.synchronize()
         print("profile: 15 prefill calls", flush=True)
+    if not args.no_pre_attention:
+        from mini_llm_runtime_amd.kernels import pre_attention as kpre
+        from mini_llm_runtime_amd.model.qwen2_attention import Qwen2RotaryEmbedding
+        pcache = PagedKVCache(1, 4096, 16, 2, 64, dtype=torch.bfloat16, device=device)
+        inv_freq = Qwen2RotaryEmbedding(64, 1_000_000.0).inv_freq.to(device)
+        gen = torch.Generator().manual_seed(2048)
+        qkv = torch.randn(2048, 18 * 64, generator=gen).to(torch.bfloat16).to(device)
+        pos = torch.randint(0, 4096, (2048,), generator=gen).to(device)
+        pslots = torch.randperm(4096 * 16, generator=gen)[:2048].to(device)
+        for _ in range(20):
+            kpre.qkv_rope_write(qkv, pos, inv_freq, pcache, 0, pslots, 14)
+        # Duration against token count (told apart by grid size in the trace).
+        for tokens in (1, 48, 512, 8192, 32768):
+            g = torch.Generator().manual_seed(tokens)
+            x = torch.randn(tokens, 18 * 64, generator=g).to(torch.bfloat16).to(device)
+            p_t = torch.randint(0, 4096, (tokens,), generator=g).to(device)
+            s_t = torch.randint(0, 4096 * 16, (tokens,), generator=g).to(device)
+            for _ in range(10):
+                kpre.qkv_rope_write(x, p_t, inv_freq, pcache, 0, s_t, 14)
+        torch.cuda.synchronize()
+        print("profile: 20 fused pre-attention calls (2048 tokens), 10 each at "
+              "1/48/512/8192/32768 tokens", flush=True)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -268,6 +292,80 @@ def bench_prefill(device, reps=4, calls_per_graph=10):
         "best_tile": best_tile,
         "tflops": flops / results[best_tile] / 1e12,
         "wl": wl,
+    }
+
+
+def bench_pre_attention(device, reps=4, calls_per_graph=10):
+    """The step before attention at a Qwen2.5-0.5B layer (hidden 896, 14/2
+    heads, head_dim 64, BF16) for a decode batch (48 tokens) and a prefill
+    step (2048 tokens): the fused mlr_qkv_rope_write kernel alone, the fused
+    step (one GEMM over the concatenated projections + the kernel), and the
+    reference's unfused sequence (three projection GEMMs, rotary embedding in
+    PyTorch ops, then the KV write)."""
+    import types
+
+    import torch
+
+    from mini_llm_runtime_amd.kernels import pre_attention as kpre
+    from mini_llm_runtime_amd.model.qwen2_attention import Qwen2Attention
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+
+    cfg = types.SimpleNamespace(hidden_size=896, num_attention_heads=14, num_key_value_heads=2,
+                                head_dim=64, rope_theta=1_000_000.0)
+    torch.manual_seed(0)
+    attn = Qwen2Attention(cfg).to(device=device, dtype=torch.bfloat16)
+    cache = PagedKVCache(1, 4096, 16, 2, 64, dtype=torch.bfloat16, device=device)
+    inv_freq = attn.rotary_embedding.inv_freq
+    bytes_per_token = 2 * (14 + 2 * 2) * 64 + 2 * 14 * 64 + 2 * 2 * 2 * 64 + 8 + 8
+    stream = torch.cuda.Stream(device)
+
+    def graph_us(fn):
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(calls_per_graph):
+                fn()
+        g.replay()
+        return timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
+
+    out = {}
+    for tokens in (48, 2048):
+        gen = torch.Generator().manual_seed(tokens)
+        hidden = torch.randn(tokens, 896, generator=gen).to(torch.bfloat16).to(device)
+        positions = torch.randint(0, 4096, (tokens,), generator=gen).to(device)
+        slots = torch.randperm(cache.num_blocks * 16, generator=gen)[:tokens].to(device)
+        weight, bias = attn._qkv_weights()
+        qkv = torch.nn.functional.linear(hidden, weight, bias)
+
+        def kernel():
+            kpre.qkv_rope_write(qkv, positions, inv_freq, cache, 0, slots, 14)
+
+        def fused():
+            attn._fused_qkv_rope_write(hidden, positions, cache, 0, slots)
+
+        def unfused():
+            _, k, v = attn._qkv_rope(hidden.unsqueeze(0), positions.unsqueeze(0))
+            cache.write_slots(slots, k[0], v[0], 0, validate=False)
+
+        k_us = graph_us(kernel)
+        out[str(tokens)] = {
+            "fused_kernel_us": round(k_us, 3),
+            "fused_step_us": round(graph_us(fused), 3),
+            "unfused_step_us": round(graph_us(unfused), 3),
+            "kernel_bytes": tokens * bytes_per_token,
+            "kernel_GBps": round(tokens * bytes_per_token / k_us / 1e3, 1),
+        }
+    big = out["2048"]
+    return {
+        "workload": "qwen05b_layer_pre_attention_bf16",
+        "by_tokens": out,
+        "roofline": {"bound": "hbm", "kernel": "mlr_qkv_rope_write (2048 tokens)",
+                     "achieved": big["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(big["kernel_GBps"] / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes_per_launch": big["kernel_bytes"]},
     }
 
 
@@ -473,6 +571,10 @@ def main():
             "us_per_call_by_kv_tile": pre["us_per_call"],
             "cpu_baseline": cpu_pre,
         }
+    if not args.no_pre_attention:
+        line["pre_attention"] = bench_pre_attention(device)
+        line["pre_attention"]["roofline"]["traffic"] = (
+            traffic.get("pre_attention_call_bytes") if traffic else None)
     if not args.no_serving:
         line["serving"] = bench_serving(device)
     print(json.dumps(line), flush=True)

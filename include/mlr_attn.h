@@ -201,6 +201,37 @@ int mlr_paged_prefill_chunk(const void *q, int64_t q_stride_t,
                             void *out, int64_t out_stride_t,
                             int64_t out_stride_h, void *stream);
 
+/*
+ * Fused pre-attention step of one layer: optional projection bias, rotary
+ * embedding of the q and k heads, and the KV-cache write, in one launch.
+ *
+ * Replaces, after the QKV projection GEMM, the bias of Qwen2QKVProjection
+ * (model/qwen2.py:211-236), Qwen2RotaryEmbedding + apply_rotary_pos_emb
+ * (:125-209, called at :605-607 and :737-739) and kv_cache.write_slots
+ * (:608-613, :741-746; runtime/paged_kv_cache.py:243-249). Rounding follows
+ * the reference operation by operation in the model dtype: f = float(pos) *
+ * inv_freq[i] in FP32; c, s = dtype(cos f), dtype(sin f); each product and the
+ * sum rounded to dtype (FP32 without fma contraction).
+ *   qkv          : [num_tokens, (num_q_heads + 2 num_kv_heads) * head_dim], row
+ *                  stride qkv_stride_t, heads in the order q, k, v, unit stride
+ *   bias         : [(num_q_heads + 2 num_kv_heads) * head_dim] or NULL; added
+ *                  (then rounded to dtype) before the rotation
+ *   positions    : int64 [num_tokens]
+ *   inv_freq     : FP32 [head_dim / 2], the rotary module's inverse frequencies
+ *   slot_mapping : int32/int64 [num_tokens]; a slot outside [0, num_slots) is
+ *                  not written (q is)
+ *   q_out        : [num_tokens, num_q_heads, head_dim], row stride q_out_stride_t
+ *   k_cache, v_cache : one layer, [num_slots / block_size, block_size,
+ *                  num_kv_heads, head_dim] contiguous
+ * qkv, bias, q_out and the cache share dtype (F32, F16 or BF16).
+ */
+int mlr_qkv_rope_write(const void *qkv, int64_t qkv_stride_t, const void *bias,
+                       const int64_t *positions, const float *inv_freq,
+                       const void *slot_mapping, int index_dtype, void *q_out,
+                       int64_t q_out_stride_t, void *k_cache, void *v_cache,
+                       int64_t num_slots, int64_t num_tokens, int64_t num_q_heads,
+                       int64_t num_kv_heads, int64_t head_dim, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,12 @@ _PROTOTYPES = {
          _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_f64, _c_int,
          _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr],
     ),
+    "mlr_qkv_rope_write": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr,
+         _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_int, _c_ptr],
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_PROTOTYPES)

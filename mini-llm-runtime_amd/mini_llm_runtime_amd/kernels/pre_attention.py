@@ -1,0 +1,87 @@
+"""Fused pre-attention step: projection bias, rotary embedding, KV-cache write.
+
+``qkv_rope_write`` takes the output of one QKV projection GEMM over the
+concatenated [q | k | v] weights and, in one launch (``mlr_qkv_rope_write``),
+adds the optional bias, rotates the q and k heads at their positions, returns
+the rotated q and writes k and v into one layer of the paged cache. It
+replaces the reference's per-layer sequence Qwen2RotaryEmbedding ->
+apply_rotary_pos_emb -> kv_cache.write_slots (model/qwen2.py:125-209,
+:605-613, :737-746), with the same rounding in the model dtype.
+
+Checks are on shapes, dtypes and devices only; slot values are the caller's
+to validate (``PagedKVCache.check_slots`` runs the reference's write_slots
+checks). A slot outside the pool is not written.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..runtime.paged_kv_cache import PagedKVCache
+
+_SUPPORTED = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor,
+                   kv_cache: PagedKVCache, layer_idx: int, slot_mapping: torch.Tensor,
+                   num_q_heads: int, *, bias: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """qkv [T, (Hq + 2 Hkv) * D] -> rotated q [T, Hq, D]; k, v to the cache.
+
+    positions: int64 [T]; inv_freq: the rotary module's buffer [D / 2] (used
+    as FP32, exactly as the reference promotes it); slot_mapping int32/int64
+    [T]; bias [(Hq + 2 Hkv) * D] or None.
+    """
+    if layer_idx < 0 or layer_idx >= kv_cache.num_layers:
+        raise IndexError("Unexpected layer_idx")
+    hkv, d = kv_cache.num_kv_heads, kv_cache.head_dim
+    if num_q_heads <= 0 or num_q_heads % hkv != 0:
+        raise ValueError("num_q_heads must be a positive multiple of the cache's KV heads")
+    width = (num_q_heads + 2 * hkv) * d
+    if qkv.ndim != 2 or qkv.shape[1] != width:
+        raise ValueError(f"qkv must have shape [num_tokens, {width}], got {tuple(qkv.shape)}")
+    if qkv.shape[0] > 0 and qkv.stride(1) != 1:
+        raise ValueError("qkv rows must be contiguous")
+    tokens = qkv.shape[0]
+    if positions.shape != (tokens,) or positions.dtype != torch.long:
+        raise ValueError("positions must be an int64 tensor of shape [num_tokens]")
+    if slot_mapping.shape != (tokens,):
+        raise ValueError("slot_mapping must have shape [num_tokens]")
+    if slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise TypeError("slot_mapping must use an integer index dtype")
+    if inv_freq.shape != (d // 2,):
+        raise ValueError(f"inv_freq must have shape [{d // 2}]")
+    if qkv.dtype not in _SUPPORTED:
+        raise TypeError(f"qkv dtype {qkv.dtype} is not supported")
+    if qkv.dtype != kv_cache.dtype:
+        raise TypeError("qkv dtype must match the KV cache dtype")
+    if bias is not None and (bias.shape != (width,) or bias.dtype != qkv.dtype):
+        raise ValueError(f"bias must have shape [{width}] and the qkv dtype")
+    if out is None:
+        out = torch.empty((tokens, num_q_heads, d), dtype=qkv.dtype, device=qkv.device)
+    elif (out.shape != (tokens, num_q_heads, d) or out.dtype != qkv.dtype
+          or (tokens > 0 and (out.stride(2) != 1 or out.stride(1) != d))):
+        raise ValueError("out must be [num_tokens, num_q_heads, head_dim] with contiguous heads")
+    tensors = [qkv, positions, inv_freq, slot_mapping, out, kv_cache.k_cache]
+    if bias is not None:
+        tensors.append(bias)
+    device = _lib.require_hip(*tensors, what="qkv_rope_write")
+    if tokens == 0:
+        return out
+    layer_k, layer_v = kv_cache.get_layer_cache(layer_idx)
+    if not (layer_k.is_contiguous() and layer_v.is_contiguous()):
+        raise ValueError("KV cache layers must be contiguous")
+    freq = inv_freq.to(torch.float32).contiguous()
+    bias_c = bias.contiguous() if bias is not None else None
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        status = lib.mlr_qkv_rope_write(
+            qkv.data_ptr(), qkv.stride(0), bias_c.data_ptr() if bias_c is not None else None,
+            positions.data_ptr(), freq.data_ptr(), slot_mapping.data_ptr(),
+            _lib.INDEX_CODES[slot_mapping.dtype], out.data_ptr(), out.stride(0),
+            layer_k.data_ptr(), layer_v.data_ptr(), kv_cache.num_blocks * kv_cache.block_size,
+            tokens, num_q_heads, hkv, d, _lib.dtype_code(qkv.dtype, "qkv_rope_write"),
+            _lib.stream_handle(device))
+    _lib.check(status, "mlr_qkv_rope_write")
+    return out

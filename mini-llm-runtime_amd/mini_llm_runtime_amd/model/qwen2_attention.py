@@ -3,20 +3,28 @@
 The callers of the paged path in the reference (model/qwen2.py:258-767):
 ``Qwen2Attention`` and its pieces, with the same module names, construction
 order (q_proj, v_proj, k_proj, so a seeded initialisation and a reference
-state_dict both carry over), arguments, validation order and messages. The
-projections and the rotary embedding are PyTorch ops, as in the reference;
-the cache write and the attention run on the HIP library:
+state_dict both carry over), arguments, validation order and messages.
+
+On the cache paths the step before attention is fused: one projection GEMM
+over the concatenated [q | k | v] weights and biases, then one
+``mlr_qkv_rope_write`` launch that rotates q and k at their positions and
+writes k and v into the layer's cache (reference :605-613, :737-746), with
+the reference's rounding; then the attention kernel:
 
 - ``forward_decode_batch_with_cache`` validates the step's metadata with one
-  host sync, then writes the new K/V rows and decodes in one launch
-  (``mlr_paged_decode_append``), replacing the write_slots +
-  paged_attention_decode_batch_parallel pair (reference :608-621).
-- ``forward_prefill_chunk_with_cache`` writes the chunk's rows and runs the
-  tiled chunk prefill (reference :737-767).
-- ``forward_prefill_with_cache`` writes the prompt's rows and attends over
-  the fresh K/V with the chunk kernel at prefix 0, viewing them as a pool of
-  16-row blocks (the reference uses its dense attention here, :427-439).
-- ``forward_decode_with_cache`` is the single-request decode (:441-536).
+  host sync, then runs the fused step and the batched decode, replacing the
+  write_slots + paged_attention_decode_batch_parallel pair (reference
+  :608-621).
+- ``forward_prefill_packed_with_cache`` (all prefill requests of a step) runs
+  the fused step and one varlen prefill.
+- ``forward_prefill_chunk_with_cache`` runs the fused step and the tiled
+  chunk prefill (reference :737-767).
+- ``forward_prefill_with_cache`` keeps PyTorch projections and rotation,
+  writes the prompt's rows and attends over the fresh K/V with the chunk
+  kernel at prefix 0, viewing them as a pool of 16-row blocks (the reference
+  uses its dense attention here, :427-439).
+- ``forward_decode_with_cache`` is the single-request decode (:441-536), on
+  the fused step.
 
 ``forward`` (no cache) keeps the reference's dense PyTorch attention: it is
 not on the paged path.
@@ -28,6 +36,7 @@ import torch
 import torch.nn as nn
 
 from ..kernels import paged_attention as kpa
+from ..kernels import pre_attention as kpre
 from ..runtime.paged_kv_cache import PagedKVCache
 
 
@@ -145,6 +154,8 @@ class Qwen2Attention(nn.Module):
         self.rotary_embedding = Qwen2RotaryEmbedding(head_dim=config.head_dim,
                                                      theta=config.rope_theta)
         self.o_proj = nn.Linear(config.hidden_size, config.hidden_size, bias=False)
+        self._qkv_cat_key = None
+        self._qkv_cat = None
 
     # ------------------------------------------------------------------
     # Shared pieces
@@ -174,6 +185,48 @@ class Qwen2Attention(nn.Module):
         cos, sin = self.rotary_embedding(query, position_ids)
         query, key = apply_rotary_pos_emb(query, key, cos, sin)
         return query, key, value
+
+    def _qkv_weights(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """[q; k; v] projection weight and bias, concatenated once and rebuilt
+        when a projection parameter is replaced or changed in place."""
+        proj = self.qkv_proj
+        parts = (proj.q_proj.weight, proj.k_proj.weight, proj.v_proj.weight,
+                 proj.q_proj.bias, proj.k_proj.bias, proj.v_proj.bias)
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in parts)
+        if key != self._qkv_cat_key:
+            with torch.no_grad():
+                weight = torch.cat(parts[:3], dim=0)
+                bias = torch.cat(parts[3:], dim=0)
+            self._qkv_cat, self._qkv_cat_key = (weight, bias), key
+        return self._qkv_cat
+
+    @staticmethod
+    def _check_fused_inputs(hidden_states, position_ids, kv_cache, slot_mapping) -> None:
+        """write_slots' type and device checks (runtime/paged_kv_cache.py:
+        218-233), which the fused step must keep."""
+        if slot_mapping.dtype not in (torch.int32, torch.int64):
+            raise TypeError("slot_mapping must use an integer index dtype")
+        cache_device = kv_cache.k_cache.device
+        if slot_mapping.device != cache_device or hidden_states.device != cache_device:
+            raise ValueError("slot_mapping and K/V must be on the KV cache device")
+
+    def _fused_qkv_rope_write(self, hidden_2d: torch.Tensor, positions: torch.Tensor,
+                              kv_cache: PagedKVCache, layer_idx: int,
+                              slot_mapping: torch.Tensor) -> torch.Tensor:
+        """Rotated q [T, Hq, D] of the tokens hidden_2d [T, hidden]; their
+        rotated k and v are written to slot_mapping of the layer's cache.
+        A cache of another dtype than the model (write_slots converts, as in
+        the reference) or a dtype the kernel lacks takes the unfused path."""
+        if hidden_2d.dtype != kv_cache.dtype or hidden_2d.dtype not in (
+                torch.float32, torch.float16, torch.bfloat16):
+            query, key, value = self._qkv_rope(hidden_2d.unsqueeze(0), positions.unsqueeze(0))
+            kv_cache.write_slots(slot_mapping=slot_mapping, k=key[0], v=value[0],
+                                 layer_idx=layer_idx, validate=False)
+            return query[0]
+        weight, bias = self._qkv_weights()
+        qkv = torch.nn.functional.linear(hidden_2d, weight, bias)
+        return kpre.qkv_rope_write(qkv, positions.to(torch.long), self.rotary_embedding.inv_freq,
+                                   kv_cache, layer_idx, slot_mapping, self.num_attention_heads)
 
     # ------------------------------------------------------------------
     # No cache: the reference's dense attention (model/qwen2.py:282-370)
@@ -265,11 +318,12 @@ class Qwen2Attention(nn.Module):
         if position != context_len - 1:
             raise ValueError("decode position must equal context_len - 1, "
                              f"got position={position} and context_len={context_len}")
-        query, key, value = self._qkv_rope(hidden_states, position_ids)
-        kv_cache.write_slots(slot_mapping=slot_mapping, k=key.squeeze(1),
-                             v=value.squeeze(1), layer_idx=layer_idx)
+        self._check_fused_inputs(hidden_states, position_ids, kv_cache, slot_mapping)
+        kv_cache.check_slots(slot_mapping)
+        query = self._fused_qkv_rope_write(hidden_states[0], position_ids[0], kv_cache,
+                                           layer_idx, slot_mapping)
         k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)
-        out = kpa.paged_attention_decode(q=query[0, 0], k_cache=k_layer, v_cache=v_layer,
+        out = kpa.paged_attention_decode(q=query[0], k_cache=k_layer, v_cache=v_layer,
                                          block_table=block_table, seq_len=context_len,
                                          block_size=kv_cache.block_size)
         return self.o_proj(out.reshape(1, 1, self.hidden_size))
@@ -309,12 +363,11 @@ class Qwen2Attention(nn.Module):
         self._check_decode_metadata(kv_cache, position_ids, slot_mapping, block_tables,
                                     context_lens)
         k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)
-        query, key, value = self._qkv_rope(hidden_states, position_ids)
-        # Write of the new rows and decode in one launch; the metadata checks
-        # above are the ones write_slots and the decode would repeat.
-        out = kpa.paged_decode_launch(query.squeeze(1), k_layer, v_layer, block_tables,
-                                      context_lens, new_k=key.squeeze(1),
-                                      new_v=value.squeeze(1), slot_mapping=slot_mapping)
+        # The metadata checks above are the ones write_slots and the decode
+        # would repeat.
+        query = self._fused_qkv_rope_write(hidden_states[:, 0], position_ids[:, 0], kv_cache,
+                                           layer_idx, slot_mapping)
+        out = kpa.paged_decode_launch(query, k_layer, v_layer, block_tables, context_lens)
         return self.o_proj(out.reshape(batch, 1, self.hidden_size))
 
     @staticmethod
@@ -379,11 +432,11 @@ class Qwen2Attention(nn.Module):
             raise ValueError("hidden_states must have shape [num_tokens, hidden_size]")
         if position_ids.shape != hidden_states.shape[:1]:
             raise ValueError("position_ids must have shape [num_tokens]")
-        query, key, value = self._qkv_rope(hidden_states.unsqueeze(0), position_ids.unsqueeze(0))
-        kv_cache.write_slots(slot_mapping=slot_mapping, k=key.squeeze(0), v=value.squeeze(0),
-                             layer_idx=layer_idx, validate=False)
+        self._check_fused_inputs(hidden_states, position_ids, kv_cache, slot_mapping)
+        query = self._fused_qkv_rope_write(hidden_states, position_ids, kv_cache, layer_idx,
+                                           slot_mapping)
         k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)
-        out = kpa.paged_prefill_launch(query.squeeze(0).contiguous(), k_layer, v_layer,
+        out = kpa.paged_prefill_launch(query, k_layer, v_layer,
                                        block_tables, query_start_loc, context_lens,
                                        max_query_len)
         return self.o_proj(out.reshape(-1, self.hidden_size))
@@ -436,13 +489,13 @@ class Qwen2Attention(nn.Module):
         expected_slots = table_t[positions // bs] * bs + positions % bs
         if not torch.equal(slot_mapping.to(torch.long), expected_slots):
             raise ValueError("slot_mapping does not match block_table for the chunk positions")
-        query, key, value = self._qkv_rope(hidden_states, position_ids)
         # Slots are distinct and in range: they follow a validated table.
-        kv_cache.write_slots(slot_mapping=slot_mapping, k=key.squeeze(0), v=value.squeeze(0),
-                             layer_idx=layer_idx, validate=False)
+        self._check_fused_inputs(hidden_states, position_ids, kv_cache, slot_mapping)
+        query = self._fused_qkv_rope_write(hidden_states[0], position_ids[0], kv_cache,
+                                           layer_idx, slot_mapping)
         k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)
         out = kpa.paged_attention_prefill_chunk_tiled(
-            q=query.squeeze(0), k_cache=k_layer, v_cache=v_layer, block_table=table,
+            q=query, k_cache=k_layer, v_cache=v_layer, block_table=table,
             prefix_len=prefix_len, context_len=context_len, block_size=bs,
             tile_size=tile_size)
         return self.o_proj(out.reshape(1, chunk_len, self.hidden_size))

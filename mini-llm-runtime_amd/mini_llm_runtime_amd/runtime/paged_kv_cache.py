@@ -177,22 +177,28 @@ class PagedKVCache:
             raise ValueError("slot_mapping and K/V must be on the KV cache device")
         if k.dtype != v.dtype:
             raise TypeError("K and V must share one dtype")
-        num_slots = self.num_blocks * self.block_size
-        if validate and slot_mapping.numel() > 0:
-            # Both checks in one device pass and one host sync; the range
-            # check wins when both fail, as in the reference (:235-239).
-            ordered = slot_mapping.sort().values
-            flags = torch.stack([
-                ((ordered[0] < 0) | (ordered[-1] >= num_slots)),
-                (ordered[1:] == ordered[:-1]).any(),
-            ]).cpu()
-            if bool(flags[0]):
-                raise IndexError("slot_mapping contains an out-of-range slot")
-            if bool(flags[1]):
-                raise ValueError("slot_mapping must contain distinct slots")
+        if validate:
+            self.check_slots(slot_mapping)
         if k.shape[0] == 0:
             return
         self._launch_write(slot_mapping, k, v, layer_idx)
+
+    def check_slots(self, slot_mapping: torch.Tensor) -> None:
+        """The value checks of write_slots (reference :235-239): every slot in
+        range, no slot twice. Both run in one device pass and one host sync;
+        the range check wins when both fail, as in the reference."""
+        if slot_mapping.numel() == 0:
+            return
+        num_slots = self.num_blocks * self.block_size
+        ordered = slot_mapping.sort().values
+        flags = torch.stack([
+            ((ordered[0] < 0) | (ordered[-1] >= num_slots)),
+            (ordered[1:] == ordered[:-1]).any(),
+        ]).cpu()
+        if bool(flags[0]):
+            raise IndexError("slot_mapping contains an out-of-range slot")
+        if bool(flags[1]):
+            raise ValueError("slot_mapping must contain distinct slots")
 
     def _launch_write(self, slot_mapping: torch.Tensor, k: torch.Tensor,
                       v: torch.Tensor, layer_idx: int) -> None:

@@ -3,7 +3,8 @@
 Same weights on both sides (the module's own seeded initialisation, copied
 into the oracle's weight dict). Checked per method: the layer output, the K/V
 rows written to the cache, and that every other slot is left untouched
-(bit-for-bit; written slots hold exactly the module's own K/V rows).
+(bit-for-bit; written slots hold exactly the K/V rows of the module's own
+projection and rotation on the GPU).
 Tolerances on the layer output (projections, RoPE, attention, o_proj):
 1e-5 max-abs for FP32, 2e-2 for BF16.
 """
@@ -16,7 +17,7 @@ import pytest
 import torch
 
 import oracle.qwen2_attention as oqa
-from mini_llm_runtime_amd.model.qwen2_attention import Qwen2Attention
+from mini_llm_runtime_amd.model.qwen2_attention import Qwen2Attention, apply_rotary_pos_emb
 from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
 from oracle.paged_kv_cache import OracleKVCache
 
@@ -78,10 +79,26 @@ def check_caches(dev, ora, written_slots, rows_k, rows_v):
     assert torch.equal(got_v[idx], rows_v.cpu())
 
 
-def module_rows(module, hidden, positions, device):
-    """The K/V rows the module writes for these inputs, [T, Hkv, D]."""
-    _, k, v = module._qkv_rope(hidden.to(device), positions.to(device))
-    return k.reshape(-1, *k.shape[-2:]), v.reshape(-1, *v.shape[-2:])
+def module_rows(module, hidden, positions, device, fused=True):
+    """The K/V rows the module writes for these inputs, [T, Hkv, D].
+
+    The cache paths project with one GEMM over the concatenated [q | k | v]
+    weights and rotate in the fused kernel, which repeats the PyTorch
+    rotation bit for bit (tests/test_gpu_pre_attention.py); the whole-prompt
+    prefill keeps the three projections (fused=False)."""
+    hidden, positions = hidden.to(device), positions.to(device)
+    if not fused:
+        _, k, v = module._qkv_rope(hidden, positions)
+        return k.reshape(-1, *k.shape[-2:]), v.reshape(-1, *v.shape[-2:])
+    weight, bias = module._qkv_weights()
+    x = torch.nn.functional.linear(hidden.reshape(-1, hidden.shape[-1]), weight, bias)
+    hq, hkv, d = module.num_attention_heads, module.num_key_value_heads, module.head_dim
+    q = x[:, :hq * d].reshape(-1, hq, d)
+    k = x[:, hq * d:(hq + hkv) * d].reshape(-1, hkv, d)
+    v = x[:, (hq + hkv) * d:].reshape(-1, hkv, d)
+    cos, sin = module.rotary_embedding(q, positions.reshape(-1))
+    _, k = apply_rotary_pos_emb(q, k, cos, sin)
+    return k, v
 
 
 def max_abs(a, b):
@@ -182,12 +199,14 @@ def test_prefill_whole_with_cache(device, cfg, dtype, seq):
                                             slots.to(device))
     want = oqa.prefill_whole(hidden, positions, ora, 0, slots, w, oracle_cfg(cfg))
     assert max_abs(got, want) <= TOL[dtype]
-    check_caches(dev, ora, slots.tolist(), *module_rows(module, hidden, positions, device))
+    check_caches(dev, ora, slots.tolist(),
+                 *module_rows(module, hidden, positions, device, fused=False))
 
 
 def test_decode_steps_follow_the_prefill(device):
-    """Prefill a prompt, then decode three tokens, each step's K/V appended by
-    the fused decode; the whole sequence matches the oracle run step by step."""
+    """Prefill a prompt, then decode three tokens, each step's K/V written by
+    the fused pre-attention step; the whole sequence matches the oracle run
+    step by step."""
     cfg, dtype = SMALL, torch.float32
     module, w = make_module(cfg, dtype, device)
     bs, nblocks = 4, 12
@@ -203,7 +222,7 @@ def test_decode_steps_follow_the_prefill(device):
     want = oqa.prefill_whole(hidden, positions, ora, 0, slots, w, oracle_cfg(cfg))
     assert max_abs(got, want) <= TOL[dtype]
     written = slots.tolist()
-    rows = [module_rows(module, hidden, positions, device)]
+    rows = [module_rows(module, hidden, positions, device, fused=False)]
     bt = torch.tensor([table])
     for step in range(3):
         n = prompt + step + 1

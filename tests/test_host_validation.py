@@ -226,3 +226,39 @@ def test_qwen2_attention_matches_reference_state_dict_names():
         "qkv_proj.q_proj.weight", "qkv_proj.q_proj.bias", "qkv_proj.v_proj.weight",
         "qkv_proj.v_proj.bias", "qkv_proj.k_proj.weight", "qkv_proj.k_proj.bias",
         "o_proj.weight"]
+
+
+def _pre_attention_args(**over):
+    from mini_llm_runtime_amd.model.qwen2_attention import Qwen2RotaryEmbedding
+    cache = PagedKVCache(1, 4, 16, 2, 8, dtype=torch.float32)
+    args = dict(qkv=torch.randn(3, (4 + 4) * 8), positions=torch.arange(3),
+                inv_freq=Qwen2RotaryEmbedding(8).inv_freq, kv_cache=cache, layer_idx=0,
+                slot_mapping=torch.tensor([0, 5, 9]), num_q_heads=4)
+    args.update(over)
+    return args
+
+
+@pytest.mark.parametrize("over,error,message", [
+    (dict(layer_idx=1), IndexError, "layer_idx"),
+    (dict(num_q_heads=3), ValueError, "multiple"),
+    (dict(qkv=torch.randn(3, 60)), ValueError, "qkv must have shape"),
+    (dict(positions=torch.arange(3, dtype=torch.int32)), ValueError, "positions"),
+    (dict(slot_mapping=torch.tensor([0, 1])), ValueError, "slot_mapping must have shape"),
+    (dict(slot_mapping=torch.tensor([0.0, 1.0, 2.0])), TypeError, "integer"),
+    (dict(inv_freq=torch.ones(3)), ValueError, "inv_freq"),
+    (dict(qkv=torch.randn(3, 64).double()), TypeError, "not supported"),
+    (dict(qkv=torch.randn(3, 64).half()), TypeError, "KV cache dtype"),
+])
+def test_qkv_rope_write_rejects_bad_arguments(over, error, message):
+    from mini_llm_runtime_amd.kernels.pre_attention import qkv_rope_write
+    with pytest.raises(error, match=message):
+        qkv_rope_write(**_pre_attention_args(**over))
+
+
+def test_qkv_rope_write_refuses_cpu_tensors():
+    from mini_llm_runtime_amd.kernels.pre_attention import qkv_rope_write
+    args = _pre_attention_args()
+    args["kv_cache"].k_cache.fill_(5)
+    with pytest.raises(RuntimeError, match="only on HIP devices"):
+        qkv_rope_write(**args)
+    assert torch.all(args["kv_cache"].k_cache == 5)
