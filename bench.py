@@ -467,10 +467,31 @@ def bench_serving(device, steps=None):
             prefill_tokens += sum(out.num_scheduled_tokens[r.request_id]
                                   for r in out.prefill_requests)
             finished += len(result.finished_requests)
+        # Host metadata of one step: the device path build_model_batch uses
+        # (per-request host work + mlr_build_step_metadata) against the
+        # reference-style per-token host construction.
+        from mini_llm_runtime_amd.runtime.model_runner import build_model_batch
+        probe = scheduler.schedule()
+        meta = {}
+        for name, dev in (("device", device), ("host", torch.device("cpu"))):
+            build_model_batch(probe, w.block_size, dev)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(20):
+                batch = build_model_batch(probe, w.block_size, dev)
+                if dev.type == "cpu":  # the host lists still have to reach the GPU
+                    for field in ("input_token_ids", "positions", "query_start_loc",
+                                  "context_lens", "block_tables", "slot_mapping"):
+                        getattr(batch, field).to(device)
+            torch.cuda.synchronize()
+            meta[f"build_{name}_ms"] = round((time.perf_counter() - t0) / 20 * 1e3, 3)
+        meta["tokens"] = sum(probe.num_scheduled_tokens.values())
+        meta["requests"] = len(probe.scheduled_requests)
     total = sum(times)
     return {
         "workload": w.name,
         "warmup_steps": warm,
+        "step_metadata": meta,
         "steps": steps,
         "ms_per_step": round(1e3 * total / steps, 3),
         "ms_per_step_median": round(1e3 * statistics.median(times), 3),

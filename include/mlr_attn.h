@@ -232,6 +232,40 @@ int mlr_qkv_rope_write(const void *qkv, int64_t qkv_stride_t, const void *bias,
                        int64_t num_slots, int64_t num_tokens, int64_t num_q_heads,
                        int64_t num_kv_heads, int64_t head_dim, int dtype, void *stream);
 
+/*
+ * Batched weighted row sum in FP32, out[b, d] = sum_n p[b, n] * v[b, n, d],
+ * with p [batch, 64], v [batch, 64, 256] and out [batch, 256], all
+ * contiguous; v and out 16-byte aligned. Sums run in row order with fma.
+ *
+ * Replaces forward(p, v) of the reference's only native extension
+ * (kernels/cuda/paged_attention_accumulator.cu:83-100; Python wrapper
+ * kernels/cuda/accumulator.py:21-37).
+ */
+int mlr_pa_accumulate(const float *p, const float *v, float *out, int64_t batch, void *stream);
+
+/*
+ * ModelBatch metadata of one scheduler step from one row per request:
+ * req_info [num_reqs, 2] int64 holds (first position, token count) of
+ * request r, block_tables its padded block table (row stride
+ * block_table_stride, max_blocks entries used). Writes, for the packed rows,
+ *   query_start_loc [num_reqs + 1] = 0, prefix sums of the counts
+ *   context_lens    [num_reqs]     = first position + count
+ *   positions       [num_tokens]   = first position + i
+ *   slot_mapping    [num_tokens]   = block_tables[r, p / block_size] * block_size
+ *                                    + p % block_size
+ * (slot -1 where p < 0 or p / block_size >= max_blocks). The counts must be
+ * >= 0 and sum to num_tokens; num_reqs <= 16384.
+ *
+ * Replaces the per-token host loops of build_model_batch
+ * (runtime/model_runner.py:54-64 append_slots, and the position, offset and
+ * context-length lists of :66-143).
+ */
+int mlr_build_step_metadata(const int64_t *req_info, const int64_t *block_tables,
+                            int64_t block_table_stride, int64_t max_blocks, int64_t num_reqs,
+                            int64_t num_tokens, int64_t block_size, int64_t *positions,
+                            int64_t *slot_mapping, int64_t *query_start_loc,
+                            int64_t *context_lens, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

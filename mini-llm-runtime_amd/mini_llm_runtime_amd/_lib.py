@@ -79,6 +79,12 @@ _PROTOTYPES = {
          _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_int, _c_ptr],
     ),
+    "mlr_pa_accumulate": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr]),
+    "mlr_build_step_metadata": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,
+         _c_ptr, _c_ptr, _c_ptr],
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_PROTOTYPES)

@@ -50,42 +50,36 @@ class GenerationStepResult:
     finished_requests: list[Request]
 
 
-def _slots(request: Request, start: int, count: int, block_size: int) -> list[int]:
-    table = request.block_table
+def _check_blocks(request: Request, start: int, count: int, block_size: int) -> None:
+    """The table must cover every scheduled position (reference :54-64)."""
     last = start + count - 1
-    if count > 0 and last // block_size >= len(table):
+    if count > 0 and last // block_size >= len(request.block_table):
         # The first position without a block, as the reference reports it.
-        missing = max(start, len(table) * block_size)
+        missing = max(start, len(request.block_table) * block_size)
         raise ValueError(f"Request {request.request_id} has no KV cache block "
                          f"for position {missing}")
+
+
+def _slots(request: Request, start: int, count: int, block_size: int) -> list[int]:
+    _check_blocks(request, start, count, block_size)
+    table = request.block_table
     return [table[p // block_size] * block_size + p % block_size
             for p in range(start, start + count)]
 
 
 def build_model_batch(scheduler_output: SchedulerOutput, block_size: int,
                       device: torch.device | str = "cpu") -> ModelBatch:
+    """The step's packed inputs: prefill requests first, then decodes.
+
+    On a HIP device the host does per-request work only (the reference's
+    checks, the token ids, one (first position, count) pair and the padded
+    block table per request), moves it in one copy, and one
+    mlr_build_step_metadata launch expands positions, slot_mapping,
+    query_start_loc and context_lens on the device. Other devices get the
+    same tensors built on the host."""
     if block_size <= 0:
         raise ValueError("block_size must be greater than 0")
-    ids: list[str] = []
-    phases: list[RequestStatus] = []
-    tokens: list[int] = []
-    positions: list[int] = []
-    qsl = [0]
-    ctx: list[int] = []
-    tables: list[list[int]] = []
-    slots: list[int] = []
-
-    def add(request: Request, phase: RequestStatus, new_tokens: list[int], start: int):
-        count = len(new_tokens)
-        slots.extend(_slots(request, start, count, block_size))
-        ids.append(request.request_id)
-        phases.append(phase)
-        tokens.extend(new_tokens)
-        positions.extend(range(start, start + count))
-        qsl.append(qsl[-1] + count)
-        ctx.append(start + count)
-        tables.append(list(request.block_table))
-
+    entries: list[tuple[Request, RequestStatus, list[int], int]] = []
     for request in scheduler_output.prefill_requests:
         count = scheduler_output.num_scheduled_tokens[request.request_id]
         start = request.num_computed_tokens
@@ -93,17 +87,37 @@ def build_model_batch(scheduler_output: SchedulerOutput, block_size: int,
         if len(chunk) != count:
             raise ValueError(f"Request {request.request_id} expected {count} prefill "
                              f"tokens, got {len(chunk)}")
-        add(request, RequestStatus.PREFILLING, chunk, start)
-
+        _check_blocks(request, start, count, block_size)
+        entries.append((request, RequestStatus.PREFILLING, chunk, start))
     for request in scheduler_output.decode_requests:
         if scheduler_output.num_scheduled_tokens[request.request_id] != 1:
             raise ValueError("Decode currently supports exactly one token per request")
         pending = request.pending_token_id
         if pending is None:
             raise ValueError(f"Decode request {request.request_id} has no pending token")
-        add(request, RequestStatus.DECODING, [pending], request.num_computed_tokens)
-
+        _check_blocks(request, request.num_computed_tokens, 1, block_size)
+        entries.append((request, RequestStatus.DECODING, [pending],
+                        request.num_computed_tokens))
     dev = torch.device(device)
+    if dev.type == "cuda" and entries:
+        return _build_on_device(entries, block_size, dev)
+    return _build_on_host(entries, block_size, dev)
+
+
+def _build_on_host(entries, block_size: int, dev: torch.device) -> ModelBatch:
+    tokens: list[int] = []
+    positions: list[int] = []
+    qsl = [0]
+    ctx: list[int] = []
+    slots: list[int] = []
+    for request, _, new_tokens, start in entries:
+        count = len(new_tokens)
+        slots.extend(_slots(request, start, count, block_size))
+        tokens.extend(new_tokens)
+        positions.extend(range(start, start + count))
+        qsl.append(qsl[-1] + count)
+        ctx.append(start + count)
+    tables = [list(e[0].block_table) for e in entries]
     width = max((len(t) for t in tables), default=0)
     padded = [t + [-1] * (width - len(t)) for t in tables]
 
@@ -111,15 +125,63 @@ def build_model_batch(scheduler_output: SchedulerOutput, block_size: int,
         return torch.tensor(values, dtype=torch.long, device=dev)
 
     return ModelBatch(
-        request_ids=ids,
+        request_ids=[e[0].request_id for e in entries],
         input_token_ids=long(tokens),
         positions=long(positions),
         query_start_loc=long(qsl),
-        request_phases=phases,
+        request_phases=[e[1] for e in entries],
         context_lens=long(ctx),
         block_tables=long(padded) if tables else torch.empty((0, 0), dtype=torch.long,
                                                               device=dev),
         slot_mapping=long(slots),
+    )
+
+
+def _build_on_device(entries, block_size: int, dev: torch.device) -> ModelBatch:
+    import numpy as np
+
+    from .. import _lib
+
+    num_reqs = len(entries)
+    counts = [len(e[2]) for e in entries]
+    num_tokens = sum(counts)
+    width = max(len(e[0].block_table) for e in entries)
+    # One host buffer: token ids, then (first position, count) per request,
+    # then the block tables padded with -1.
+    host = np.empty(num_tokens + 2 * num_reqs + num_reqs * width, dtype=np.int64)
+    tok = host[:num_tokens]
+    info = host[num_tokens:num_tokens + 2 * num_reqs].reshape(num_reqs, 2)
+    tab = host[num_tokens + 2 * num_reqs:].reshape(num_reqs, width)
+    tab.fill(-1)
+    at = 0
+    for i, (request, _, new_tokens, start) in enumerate(entries):
+        tok[at:at + counts[i]] = new_tokens
+        at += counts[i]
+        info[i, 0] = start
+        info[i, 1] = counts[i]
+        tab[i, :len(request.block_table)] = request.block_table
+    buf = torch.from_numpy(host).to(dev)
+    out = torch.empty(2 * num_tokens + 2 * num_reqs + 1, dtype=torch.long, device=dev)
+    positions, slots = out[:num_tokens], out[num_tokens:2 * num_tokens]
+    qsl = out[2 * num_tokens:2 * num_tokens + num_reqs + 1]
+    ctx = out[2 * num_tokens + num_reqs + 1:]
+    tables = buf[num_tokens + 2 * num_reqs:].view(num_reqs, width)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        status = lib.mlr_build_step_metadata(
+            buf[num_tokens:].data_ptr(), tables.data_ptr(), width, width, num_reqs,
+            num_tokens, block_size, positions.data_ptr(), slots.data_ptr(), qsl.data_ptr(),
+            ctx.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(status, "mlr_build_step_metadata")
+    return ModelBatch(
+        request_ids=[e[0].request_id for e in entries],
+        input_token_ids=buf[:num_tokens],
+        positions=positions,
+        query_start_loc=qsl,
+        request_phases=[e[1] for e in entries],
+        context_lens=ctx,
+        block_tables=tables,
+        slot_mapping=slots,
     )
 
 

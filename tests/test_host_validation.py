@@ -262,3 +262,13 @@ def test_qkv_rope_write_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="only on HIP devices"):
         qkv_rope_write(**args)
     assert torch.all(args["kv_cache"].k_cache == 5)
+
+
+@pytest.mark.parametrize("p,v,error,message", [
+    (torch.randn(2, 64), torch.randn(2, 64, 256), ValueError, "CUDA tensors"),
+])
+def test_accumulator_rejects_cpu_tensors(p, v, error, message):
+    # kernels/cuda/accumulator.py:25-36 of the reference: the same checks.
+    from mini_llm_runtime_amd.kernels.accumulator import paged_attention_accumulator_cuda
+    with pytest.raises(error, match=message):
+        paged_attention_accumulator_cuda(p, v)
