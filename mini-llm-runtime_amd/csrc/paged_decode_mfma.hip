@@ -74,6 +74,16 @@ __device__ __forceinline__ uint32_t vword(const typename VRow<D>::type &v, int c
   }
 }
 
+// c ? a : b for the HIP vector structs, as a select of native vectors (a
+// ternary on the structs themselves goes through stack copies).
+template <typename T>
+__device__ __forceinline__ T select_vec(bool c, const T &a, const T &b) {
+  typedef uint32_t words_t __attribute__((ext_vector_type(sizeof(T) / 4)));
+  const words_t wa = __builtin_bit_cast(words_t, a), wb = __builtin_bit_cast(words_t, b);
+  const words_t m = c ? ~words_t(0) : words_t(0);
+  return __builtin_bit_cast(T, (wa & m) | (wb & ~m));
+}
+
 // Registers of one loaded tile. blk and rel are wave-uniform.
 template <int D>
 struct Tile {
@@ -81,6 +91,7 @@ struct Tile {
   typename VRow<D>::type v[4];
   int blk;  // physical block id, -1 when the tile is absent or invalid
   int rel;  // position of the tile's first token relative to the split start
+  int sub;  // row (0..15) whose K/V the appended token replaces, or -1
 };
 
 template <int D>
@@ -114,6 +125,7 @@ __device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
   using VT = typename VRow<D>::type;
   t.blk = blk;
   t.rel = rel;
+  t.sub = -1;
   if (blk >= 0) {
     const uint32_t bytes = static_cast<uint32_t>(block_elems * 2);
     const __amdgpu_buffer_rsrc_t rk = block_rsrc(kc + (int64_t)blk * block_elems, bytes);
@@ -135,14 +147,31 @@ __device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
   }
 }
 
-template <int D>
+// With kAppend, row t.sub of the tile (if any) takes the appended token's K
+// and V rows, staged in LDS (new_row: K row then V row), in place of what was
+// read from the cache; the substitution is a per-lane select at compute time,
+// so it never waits on the tile's loads and holds no registers before.
+template <int D, bool kAppend>
 __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
                                              const bf16x8_t *qf, float scale,
-                                             int live, int g) {
+                                             int live, int g, int m16,
+                                             const uint16_t *new_row) {
   constexpr int QK = D / 32, VC = D / 16;
   using VT = typename VRow<D>::type;
   if (t.blk < 0) return;  // absent tile or invalid block id: no keys (uniform)
   const int lim = live - t.rel;  // tokens of this tile inside the context
+  if constexpr (kAppend) {
+    if (t.sub >= 0) {  // uniform
+      const bool k_row = m16 == t.sub;
+#pragma unroll
+      for (int j = 0; j < QK; ++j)
+        t.k[j] = select_vec(k_row, *reinterpret_cast<const uint4 *>(new_row + 32 * j + 8 * g),
+                            t.k[j]);
+      const VT vrow = *reinterpret_cast<const VT *>(new_row + D + VC * m16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t.v[i] = select_vec(4 * g + i == t.sub, vrow, t.v[i]);
+    }
+  }
 
   f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -224,23 +253,10 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
     return idx < p.max_blocks ? bt_row[idx] : int64_t(-1);
   };
   int64_t blk_raw = raw_block_id(lane);
-  // Fused KV write: this lane's fragments of the new token's K and V rows and
-  // its slot, loaded with the rest of the prologue (used by at most one wave).
-  using VTa = typename VRow<D>::type;
-  uint4 new_kf[QK];
-  VTa new_vf{};
-  int64_t new_slot = -1;
-  if constexpr (kAppend) {
-    const uint16_t *nk_row = static_cast<const uint16_t *>(p.new_k) + b * p.new_sb +
-                             (int64_t)kvh * p.new_sh;
-    const uint16_t *nv_row = static_cast<const uint16_t *>(p.new_v) + b * p.new_sb +
-                             (int64_t)kvh * p.new_sh;
-#pragma unroll
-    for (int j = 0; j < QK; ++j)
-      new_kf[j] = *reinterpret_cast<const uint4 *>(nk_row + 32 * j + 8 * g);
-    new_vf = *reinterpret_cast<const VTa *>(nv_row + VC * m16);
-    new_slot = p.new_slots[b];
-  }
+  // Fused KV write: the new token's slot comes with the prologue; its K/V
+  // rows are staged in LDS by the workgroup that holds the token.
+  __shared__ __align__(16) uint16_t new_row_s[2 * D];
+  const int64_t new_slot = kAppend ? p.new_slots[b] : -1;
 
   const int64_t cap = p.max_blocks * p.block_size;
   const int64_t ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
@@ -291,28 +307,32 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   const bool append_here = kAppend && last_pos >= t0 && last_pos < t1;
   const int last_rel = static_cast<int>(last_pos - t0) & ~15;  // tile of ctx - 1
   const int last_tok = static_cast<int>(last_pos - t0) & 15;   // its row
-  auto append_token = [&](Tile<D> &t, int blk) {
-    const int64_t num_slots = p.num_blocks * p.block_size;
-    const bool slot_ok = new_slot >= 0 && new_slot < num_slots;
+  // Wave 0 of the workgroup that holds the new token copies its K and V rows
+  // to slot new_slots[b] and to LDS (16 bytes per lane); the barrier publishes
+  // them. Called once, after the first batch of tile loads is issued.
+  auto stage_new_row = [&]() {
+    if (w == 0 && lane < D / 4) {
+      const bool is_v = lane >= D / 8;
+      const int off = 8 * (is_v ? lane - D / 8 : lane);
+      const uint16_t *src = static_cast<const uint16_t *>(is_v ? p.new_v : p.new_k) +
+                            b * p.new_sb + (int64_t)kvh * p.new_sh + off;
+      const uint4 x = *reinterpret_cast<const uint4 *>(src);
+      *reinterpret_cast<uint4 *>(new_row_s + (is_v ? D : 0) + off) = x;
+      const int64_t num_slots = p.num_blocks * p.block_size;
+      if (new_slot >= 0 && new_slot < num_slots) {
+        uint16_t *dst = static_cast<uint16_t *>(is_v ? p.vc_w : p.kc_w) +
+                        (new_slot * p.hkv + kvh) * D + off;
+        *reinterpret_cast<uint4 *>(dst) = x;
+      }
+    }
+    __syncthreads();
+  };
+  // Marks row last_tok of the new token's tile for substitution when the
+  // new slot is the one position ctx - 1 maps to.
+  auto mark_new_row = [&](Tile<D> &t) {
     const bool same_slot =
-        blk >= 0 && new_slot == (int64_t)blk * p.block_size + last_pos % p.block_size;
-    uint16_t *kd = static_cast<uint16_t *>(p.kc_w) + (new_slot * p.hkv + kvh) * D;
-    uint16_t *vd = static_cast<uint16_t *>(p.vc_w) + (new_slot * p.hkv + kvh) * D;
-    if (m16 == last_tok) {  // lanes holding K row last_tok
-#pragma unroll
-      for (int j = 0; j < QK; ++j) {
-        if (slot_ok) *reinterpret_cast<uint4 *>(kd + 32 * j + 8 * g) = new_kf[j];
-        if (same_slot) t.k[j] = new_kf[j];
-      }
-    }
-    if (g == (last_tok >> 2)) {  // lanes holding V row last_tok (register last_tok & 3)
-      if (slot_ok) *reinterpret_cast<VTa *>(vd + VC * m16) = new_vf;
-      if (same_slot) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (i == (last_tok & 3)) t.v[i] = new_vf;
-      }
-    }
+        t.blk >= 0 && new_slot == (int64_t)t.blk * p.block_size + last_pos % p.block_size;
+    if (same_slot) t.sub = last_tok;
   };
 
   auto issue = [&](Tile<D>(&buf)[kBatch], int kb) {
@@ -325,19 +345,30 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
       // Byte offset of the tile's first token inside its block.
       const int tile_off = static_cast<int>((t0 + rel) % p.block_size) * row_elems * 2;
       load_tile<D>(buf[u], kc, vc, block_elems, tile_off, blk, rel, lo);
-      if (append_here && k < nk && rel == last_rel) append_token(buf[u], blk);
+    }
+    if (append_here) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int k = kb + u;
+        if (k < nk && 16 * (w + kWaves * k) == last_rel) mark_new_row(buf[u]);
+      }
     }
   };
   auto compute = [&](Tile<D>(&buf)[kBatch]) {
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) compute_tile<D>(st, buf[u], qf, scale, live, g);
+    for (int u = 0; u < kBatch; ++u)
+      compute_tile<D, kAppend>(st, buf[u], qf, scale, live, g, m16, new_row_s);
   };
 
+  // The workgroup holding the new token stages its rows once, after every
+  // wave's first batch of loads is in flight (all four waves pass the
+  // barrier, with or without tiles).
   if constexpr (kDouble) {
     // Next batch in flight while the current one computes.
+    Tile<D> bufA[kBatch], bufB[kBatch];
+    if (nk > 0) issue(bufA, 0);
+    if (append_here) stage_new_row();
     if (nk > 0) {
-      Tile<D> bufA[kBatch], bufB[kBatch];
-      issue(bufA, 0);
       for (int kb = 0; kb < nk; kb += 2 * kBatch) {
         if (kb + kBatch < nk) issue(bufB, kb + kBatch);
         compute(bufA);
@@ -348,8 +379,10 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
     }
   } else {
     Tile<D> buf[kBatch];
+    if (nk > 0) issue(buf, 0);
+    if (append_here) stage_new_row();
     for (int kb = 0; kb < nk; kb += kBatch) {
-      issue(buf, kb);
+      if (kb > 0) issue(buf, kb);
       compute(buf);
     }
   }
