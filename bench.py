@@ -369,6 +369,34 @@ def bench_pre_attention(device, reps=4, calls_per_graph=10):
     }
 
 
+def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=10):
+    """The CUDA accumulator extension's contract (p [B, 64], v [B, 64, 256],
+    FP32) on mlr_pa_accumulate at the reference test's largest batch."""
+    import torch
+
+    from mini_llm_runtime_amd.kernels.accumulator import paged_attention_accumulator_cuda
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(0)
+    p = torch.randn(batch, 64, device=device, generator=gen)
+    v = torch.randn(batch, 64, 256, device=device, generator=gen)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        paged_attention_accumulator_cuda(p, v)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(calls_per_graph):
+            paged_attention_accumulator_cuda(p, v)
+    g.replay()
+    us = timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
+    nbytes = batch * (64 * 256 + 64 + 256) * 4
+    return {"workload": f"accumulator_b{batch}_n64_d256_fp32", "us": round(us, 3),
+            "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+            "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline_decode(wl, budget):
     import torch
 
@@ -596,6 +624,7 @@ def main():
         line["pre_attention"] = bench_pre_attention(device)
         line["pre_attention"]["roofline"]["traffic"] = (
             traffic.get("pre_attention_call_bytes") if traffic else None)
+    line["accumulator"] = bench_accumulator(device)
     if not args.no_serving:
         line["serving"] = bench_serving(device)
     print(json.dumps(line), flush=True)
