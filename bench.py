@@ -369,6 +369,56 @@ def bench_pre_attention(device, reps=4, calls_per_graph=10):
     }
 
 
+SPLITS_32K = (0, 4, 8, 16, 32, 64)
+
+
+def bench_decode_32k(device, reps=4, calls_per_graph=5):
+    """Long-context split-KV decode, bf16_decode_qwen7b_32k: 8 sequences of
+    32,768 tokens, 28 q / 4 KV heads, head_dim 128 (537 MB of K/V, above the
+    256 MB MALL), with the step's KV write folded in. Swept over 4/8/16/32
+    splits per sequence and the library's default split size."""
+    import torch
+
+    from mini_llm_runtime_amd import workloads
+    from mini_llm_runtime_amd.kernels import paged_attention as kpa
+
+    wl = workloads.bf16_decode_qwen7b_32k()
+    kc, vc = wl.k_cache.to(device), wl.v_cache.to(device)
+    q, bt, ctx = wl.q.to(device), wl.block_tables.to(device), wl.context_lens.to(device)
+    slots, new_k, new_v = (t.to(device) for t in (wl.slot_mapping, wl.new_k, wl.new_v))
+    out = torch.empty_like(q)
+    stream = torch.cuda.Stream(device)
+    nbytes = wl.algorithmic_bytes() + wl.write_bytes()
+    sweep = {}
+    for splits in SPLITS_32K:
+        ts = 0 if splits == 0 else 32768 // splits
+        ws = torch.empty(kpa.decode_workspace_bytes(8, 28, 128, bt.shape[1] * 16,
+                                                    torch.bfloat16, ts),
+                         dtype=torch.uint8, device=device)
+
+        def step():
+            kpa.paged_decode_launch(q, kc, vc, bt, ctx, out, tokens_per_split=ts,
+                                    workspace=ws, new_k=new_k, new_v=new_v,
+                                    slot_mapping=slots)
+
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(calls_per_graph):
+                step()
+        g.replay()
+        us = timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
+        sweep["default" if splits == 0 else str(splits)] = round(us, 2)
+    best = min(sweep, key=sweep.get)
+    best_us = sweep[best]
+    return {"workload": wl.name, "step_bytes": nbytes, "us_by_splits": sweep,
+            "best": best, "GBps": round(nbytes / best_us / 1e3, 1),
+            "frac_of_hbm_peak": round(nbytes / best_us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=10):
     """The CUDA accumulator extension's contract (p [B, 64], v [B, 64, 256],
     FP32) on mlr_pa_accumulate at the reference test's largest batch."""
@@ -624,6 +674,7 @@ def main():
         line["pre_attention"] = bench_pre_attention(device)
         line["pre_attention"]["roofline"]["traffic"] = (
             traffic.get("pre_attention_call_bytes") if traffic else None)
+    line["decode_32k"] = bench_decode_32k(device)
     line["accumulator"] = bench_accumulator(device)
     if not args.no_serving:
         line["serving"] = bench_serving(device)

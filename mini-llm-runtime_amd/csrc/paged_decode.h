@@ -45,7 +45,7 @@ struct DecodeWorkspace {
   int64_t total;
 };
 
-int64_t default_tokens_per_split(int dtype, int64_t head_dim);
+int64_t default_tokens_per_split(bool mfma, int64_t max_context);
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype);
 

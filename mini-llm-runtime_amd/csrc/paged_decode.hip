@@ -215,12 +215,16 @@ int launch_combine(const DecodeParams &p, hipStream_t stream) {
 
 template int launch_combine<bf16_t>(const DecodeParams &, hipStream_t);
 
-int64_t default_tokens_per_split(int dtype, int64_t head_dim) {
-  // 256 tokens = 16 tiles: four per wave of the MFMA kernel, which loads them
-  // in one batch; the generic kernel holds a split's scores in LDS.
-  (void)dtype;
-  (void)head_dim;
-  return 256;
+int64_t default_tokens_per_split(bool mfma, int64_t max_context) {
+  // Generic kernel: 256 tokens, whose scores it holds in LDS. Matrix-core
+  // kernel: at least 256 tokens (16 tiles, four per wave, loaded in one
+  // batch), and at most 16 splits per sequence: long contexts then get fewer,
+  // longer splits (measured at 8 x 32K tokens: 133 us with 128 splits,
+  // 108-111 us with 8-16), and the combine merges every sequence in one
+  // 16-split chunk.
+  if (!mfma) return 256;
+  const int64_t per16 = ceil_div(max_context, 16);
+  return per16 <= 256 ? 256 : ceil_div(per16, 256) * 256;
 }
 
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
@@ -246,9 +250,10 @@ extern "C" size_t mlr_paged_decode_workspace_size(int64_t batch,
                                                   int dtype) {
   if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_context <= 0)
     return 0;
-  const int64_t ts = tokens_per_split > 0
-                         ? tokens_per_split
-                         : default_tokens_per_split(dtype, head_dim);
+  // The default is sized for 256-token splits, the most splits either kernel
+  // uses by default, so it covers whichever kernel the call takes.
+  (void)head_dim;
+  const int64_t ts = tokens_per_split > 0 ? tokens_per_split : 256;
   const int64_t splits = ceil_div(max_context, ts);
   return static_cast<size_t>(
       decode_workspace_layout(batch, num_q_heads, head_dim, splits, dtype).total);
@@ -302,7 +307,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
       aligned && decode_mfma_eligible(dtype, head_dim,
                                       num_q_heads / num_kv_heads, block_size);
   int64_t ts = tokens_per_split > 0 ? tokens_per_split
-                                    : default_tokens_per_split(dtype, head_dim);
+                                    : default_tokens_per_split(mfma, max_context);
   if (!mfma) {
     MLR_REQUIRE(ts <= kGenMaxSplit,
                 "mlr_paged_decode: tokens_per_split %lld exceeds %d for this "
