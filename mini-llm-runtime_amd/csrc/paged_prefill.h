@@ -28,6 +28,8 @@ struct PrefillParams {
   int kv_tile;
   int bs_log2;  // log2(block_size) when it is a power of two, else -1
   int n_qtiles; // query tiles per sequence (matrix-core kernel only)
+  int ncu;      // compute units of the device (matrix-core kernel only)
+  int pair_cu;  // 1: the launch fits two workgroups per CU (matrix-core kernel)
   void *out;
   int64_t o_st, o_sh;
 };

@@ -118,6 +118,16 @@ __device__ __forceinline__ int64_t uniform64(int64_t x) {
 // take the k-th contiguous share of the tiles for the same 128 queries, and
 // the splits are merged through LDS at the end. A long sequence's critical path
 // shrinks by KS.
+// Rank (0 = most keys) of the work taken by workgroup b of nwg; see the
+// kernel's prologue.
+__device__ __forceinline__ int workgroup_rank(int b, int nwg, int ncu, int pair_cu) {
+  if (!pair_cu || nwg <= ncu || b >= 2 * ncu) return b;
+  const int paired = min(nwg, 2 * ncu) - ncu;  // CUs that host two workgroups
+  const int single = ncu - paired;             // CUs that host one
+  if (b >= ncu) return single + 2 * paired - 1 - (b - ncu);  // light half, reversed
+  return b < paired ? single + b : b - paired;
+}
+
 template <int D, int BN, int KS>
 __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2)))
 void prefill_mfma(PrefillParams p) {
@@ -137,17 +147,23 @@ void prefill_mfma(PrefillParams p) {
   __shared__ __align__(8) unsigned char badk0[KS][8];
   __shared__ __align__(8) unsigned char badk1[KS][8];
 
-  // Work items are (sequence, query tile) pairs, each run once per query head.
-  // Workgroups start in order of blockIdx.x, and the hardware hands a freed
-  // CU the next one, so the items are taken longest first (list scheduling):
-  // blockIdx.x = rank * hq + head, where rank orders the items by the keys
-  // they need, longest first, ties by item index. With more than kRankMax
-  // items the ranking is skipped and items go sequence by sequence, last
-  // query tile first.
+  // Work items are (sequence, query tile) pairs, each run once per query head;
+  // a workgroup's rank wr = rank * hq + head, where rank orders the items by
+  // the keys they need, longest first, ties by item index. With more than
+  // kRankMax items the ranking is skipped and items go sequence by sequence,
+  // last query tile first.
+  // Workgroups start in order of blockIdx.x and the hardware hands a freed CU
+  // the next one. When two fit per CU, the first 2*ncu start at once, and
+  // workgroups b and b + ncu share a CU (the dispatcher deals each XCD's CUs
+  // in the same order on every pass). Those pairs get a heavy and a light
+  // rank, and CUs left with one workgroup get the heaviest; later workgroups
+  // follow in rank order (list scheduling).
   const int nqt = p.n_qtiles;
   const int nitems = p.num_seqs * nqt;
-  const int rank = static_cast<int>(blockIdx.x) / p.hq;
-  const int h = static_cast<int>(blockIdx.x) % p.hq;
+  const int wr = workgroup_rank(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x),
+                                p.ncu, p.pair_cu);
+  const int rank = wr / p.hq;
+  const int h = wr % p.hq;
   int item;
   if (nitems <= kRankMax) {
     __shared__ int item_len[kRankMax];
@@ -520,6 +536,24 @@ int launch(const PrefillParams &p, int64_t max_query_len, hipStream_t stream) {
   const int64_t blocks = static_cast<int64_t>(q.num_seqs) * q.n_qtiles * q.hq;
   if (blocks > INT32_MAX)
     return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_prefill: too many work items");
+  // CU count and workgroups per CU of this kernel, once per device.
+  constexpr int kMaxDevices = 64;
+  static int ncu_of[kMaxDevices], per_cu_of[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(MLR_ERR_HIP, "mlr_paged_prefill: no current device");
+  if (ncu_of[dev] == 0) {
+    int ncu = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(prefill_mfma<D, BN, KS>), 256 * KS, 0) !=
+            hipSuccess)
+      return set_error(MLR_ERR_HIP, "mlr_paged_prefill: device query failed");
+    per_cu_of[dev] = per_cu;
+    ncu_of[dev] = ncu;
+  }
+  q.ncu = ncu_of[dev];
+  q.pair_cu = per_cu_of[dev] == 2 ? 1 : 0;
   prefill_mfma<D, BN, KS><<<dim3(static_cast<unsigned>(blocks)), 256 * KS, 0, stream>>>(q);
   return check_launch("mlr_paged_prefill(mfma)");
 }
