@@ -221,11 +221,13 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   constexpr int QK = D / 32;
   constexpr int VC = D / 16;
 
-  // Grid (batch, KV head, split): split is the slowest dimension, so the
+  // Grid (KV head, batch, split): split is the slowest dimension, so the
   // dispatcher hands out every sequence's first split before any later one
   // and the workgroups of splits past short contexts (which exit at once)
-  // come last.
-  const int b = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
+  // come last. The KV heads of one (sequence, split) are adjacent and start
+  // together, so the halves of the same slot rows are read at about the same
+  // time (measured: 8 x 32K decode 113 -> 109 us, 4K batch-64 step -0.1 us).
+  const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
   const int lane = threadIdx.x & 63;
   // The wave index is uniform within a wave; saying so keeps every value
   // derived from it (tile counts, block ids, descriptors) in SGPRs.
@@ -505,7 +507,7 @@ bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
 }
 
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
-  dim3 grid(p.batch, p.hkv, p.max_splits);
+  dim3 grid(p.hkv, p.batch, p.max_splits);
   // Tiles per wave: ceil(ts / 16 / 4). A split whose tiles fit one load batch
   // needs no second register buffer (fewer VGPRs, more waves per SIMD).
   const int tiles_per_wave = static_cast<int>(ceil_div(ceil_div(p.ts, 16), kWaves));
