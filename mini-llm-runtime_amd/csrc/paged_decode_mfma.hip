@@ -126,23 +126,27 @@ __device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
   t.blk = blk;
   t.rel = rel;
   t.sub = -1;
-  if (blk >= 0) {
-    const uint32_t bytes = static_cast<uint32_t>(block_elems * 2);
-    const __amdgpu_buffer_rsrc_t rk = block_rsrc(kc + (int64_t)blk * block_elems, bytes);
-    const __amdgpu_buffer_rsrc_t rv = block_rsrc(vc + (int64_t)blk * block_elems, bytes);
+  // The loads are issued for absent tiles too, through an empty resource
+  // (they return zeros and touch no memory): loads under a branch would make
+  // the compiler's wait counts assume the fewest loads on any path, so the
+  // first tile would wait for nearly every load of the batch.
+  const bool ok = blk >= 0;
+  const uint32_t bytes = ok ? static_cast<uint32_t>(block_elems * 2) : 0u;
+  const int64_t base = ok ? (int64_t)blk * block_elems : 0;
+  const __amdgpu_buffer_rsrc_t rk = block_rsrc(kc + base, bytes);
+  const __amdgpu_buffer_rsrc_t rv = block_rsrc(vc + base, bytes);
 #pragma unroll
-    for (int j = 0; j < QK; ++j)
-      t.k[j] = __builtin_bit_cast(
-          uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, o.k + 64 * j, tile_off_bytes, 0));
+  for (int j = 0; j < QK; ++j)
+    t.k[j] = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, o.k + 64 * j, tile_off_bytes, 0));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (D == 64) {
-        t.v[i] = __builtin_bit_cast(
-            VT, __builtin_amdgcn_raw_buffer_load_b64(rv, o.v + i * o.v_step, tile_off_bytes, 0));
-      } else {
-        t.v[i] = __builtin_bit_cast(
-            VT, __builtin_amdgcn_raw_buffer_load_b128(rv, o.v + i * o.v_step, tile_off_bytes, 0));
-      }
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (D == 64) {
+      t.v[i] = __builtin_bit_cast(
+          VT, __builtin_amdgcn_raw_buffer_load_b64(rv, o.v + i * o.v_step, tile_off_bytes, 0));
+    } else {
+      t.v[i] = __builtin_bit_cast(
+          VT, __builtin_amdgcn_raw_buffer_load_b128(rv, o.v + i * o.v_step, tile_off_bytes, 0));
     }
   }
 }
@@ -255,10 +259,18 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
     return idx < p.max_blocks ? bt_row[idx] : int64_t(-1);
   };
   int64_t blk_raw = raw_block_id(lane);
-  // Fused KV write: the new token's slot comes with the prologue; its K/V
-  // rows are staged in LDS by the workgroup that holds the token.
+  // Fused KV write: the new token's slot and its K/V rows (wave 0, 16 bytes
+  // per lane) come with the prologue, so that staging them (LDS and cache,
+  // by the workgroup that holds the token) waits for no tile load.
   __shared__ __align__(16) uint16_t new_row_s[2 * D];
   const int64_t new_slot = kAppend ? p.new_slots[b] : -1;
+  const bool new_is_v = lane >= D / 8;
+  const int new_off = 8 * (new_is_v ? lane - D / 8 : lane);
+  uint4 new_chunk = make_uint4(0, 0, 0, 0);
+  if (kAppend && w == 0 && lane < D / 4)
+    new_chunk = *reinterpret_cast<const uint4 *>(
+        static_cast<const uint16_t *>(new_is_v ? p.new_v : p.new_k) + b * p.new_sb +
+        (int64_t)kvh * p.new_sh + new_off);
 
   const int64_t cap = p.max_blocks * p.block_size;
   const int64_t ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
@@ -314,17 +326,12 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   // them. Called once, after the first batch of tile loads is issued.
   auto stage_new_row = [&]() {
     if (w == 0 && lane < D / 4) {
-      const bool is_v = lane >= D / 8;
-      const int off = 8 * (is_v ? lane - D / 8 : lane);
-      const uint16_t *src = static_cast<const uint16_t *>(is_v ? p.new_v : p.new_k) +
-                            b * p.new_sb + (int64_t)kvh * p.new_sh + off;
-      const uint4 x = *reinterpret_cast<const uint4 *>(src);
-      *reinterpret_cast<uint4 *>(new_row_s + (is_v ? D : 0) + off) = x;
+      *reinterpret_cast<uint4 *>(new_row_s + (new_is_v ? D : 0) + new_off) = new_chunk;
       const int64_t num_slots = p.num_blocks * p.block_size;
       if (new_slot >= 0 && new_slot < num_slots) {
-        uint16_t *dst = static_cast<uint16_t *>(is_v ? p.vc_w : p.kc_w) +
-                        (new_slot * p.hkv + kvh) * D + off;
-        *reinterpret_cast<uint4 *>(dst) = x;
+        uint16_t *dst = static_cast<uint16_t *>(new_is_v ? p.vc_w : p.kc_w) +
+                        (new_slot * p.hkv + kvh) * D + new_off;
+        *reinterpret_cast<uint4 *>(dst) = new_chunk;
       }
     }
     __syncthreads();
@@ -380,8 +387,10 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
       }
     }
   } else {
+    // Issued whatever nk is (absent tiles read zeros), so that every path
+    // reaching the computes has the same loads in flight.
     Tile<D> buf[kBatch];
-    if (nk > 0) issue(buf, 0);
+    issue(buf, 0);
     if (append_here) stage_new_row();
     for (int kb = 0; kb < nk; kb += kBatch) {
       if (kb > 0) issue(buf, kb);

@@ -106,7 +106,9 @@ def test_decode_matches_oracle(device, dtype, hq, hkv, d, bs, lens):
     assert max_abs(got, want) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("tokens_per_split", [16, 48, 256, 512, 4096])
+# 272..384: splits of 5-6 tiles per wave, whose last one or two tiles go
+# through LDS (head_dim 64).
+@pytest.mark.parametrize("tokens_per_split", [16, 48, 256, 272, 320, 384, 512, 4096])
 def test_split_size_does_not_change_the_result(device, tokens_per_split):
     q, kc, vc, bt, sl, tables = random_paged([40, 777, 1500], 14, 2, 64, 16,
                                              dtype=torch.bfloat16, seed=5)
@@ -118,6 +120,7 @@ def test_split_size_does_not_change_the_result(device, tokens_per_split):
 @pytest.mark.parametrize("dtype,lens,tokens_per_split", [
     (torch.bfloat16, [1, 16, 17, 300, 1000, 257], 0),     # fused in the MFMA kernel
     (torch.bfloat16, [33, 64, 500], 64),
+    (torch.bfloat16, [300, 384, 770, 5], 384),              # new token in an LDS tile
     (torch.float32, [5, 255, 256], 0),                     # write kernel, then decode
 ])
 def test_decode_append_equals_write_then_decode(device, dtype, lens, tokens_per_split):
