@@ -11,7 +11,8 @@
 //       row slice [32j + 8(l/16), +8): the A operand comes straight from a
 //       16-byte global load, no LDS.
 //   online softmax (FP32, base-2): lane l owns head l%16 and tokens
-//       4(l/16)..+3 of the tile; the head's max is two cross-row shuffles.
+//       4(l/16)..+3 of the tile; the head's max is two lane swaps
+//       (v_permlane16_swap, v_permlane32_swap).
 //   O^T[D x 16 heads] += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
 //       v_mfma_f32_16x16x16bf16_1k, D/16 tiles. P^T is the S^T accumulator
 //       layout itself (rows 4(l/16)+i, column l%16), rounded to bf16. V is
@@ -58,6 +59,32 @@ __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
   const __bf16 b = static_cast<__bf16>(hi);
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+// Butterfly steps across lanes l ^ 16 and l ^ 32 as VALU lane swaps
+// (v_permlane16_swap / v_permlane32_swap), not LDS permutes: after the swap
+// of x with itself, the two halves of the result hold x of both partners, in
+// every lane. max and + are commutative, so the results equal those of a
+// __shfl_xor butterfly bit for bit.
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // 16-bit half `h` (0 = low, 1 = high) of word w.
@@ -189,8 +216,7 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
     x[i] = (4 * g + i < lim) ? r * kLog2e : -INFINITY;
   }
   float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = max_xor32(max_xor16(mx));
   const float m_new = fmaxf(st.m, mx);  // finite: every tile has a live token
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
   float pr[4];
@@ -399,8 +425,7 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   }
 
   // Per-head l: sum the four lanes that share the head.
-  st.l += __shfl_xor(st.l, 16);
-  st.l += __shfl_xor(st.l, 32);
+  st.l = sum_xor32(sum_xor16(st.l));
 
   __shared__ float o_s[kWaves][16][D + 4];
   __shared__ float m_s[kWaves][16];
