@@ -87,6 +87,29 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Reductions over the 16 lanes of row 0 (lanes 0..15) with DPP moves inside
+// the row (quad xor 1, quad xor 2, half-row mirror, row mirror): afterwards
+// every lane of the row holds the result. VALU only, no LDS permutes.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp_move<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = fmaxf(x, dpp_move<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = fmaxf(x, dpp_move<0x141>(x));  // row_half_mirror
+  return fmaxf(x, dpp_move<0x140>(x));  // row_mirror
+}
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp_move<0xB1>(x);
+  x += dpp_move<0x4E>(x);
+  x += dpp_move<0x141>(x);
+  return x + dpp_move<0x140>(x);
+}
+__device__ __forceinline__ float lane_value(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
 // 16-bit half `h` (0 = low, 1 = high) of word w.
 __device__ __forceinline__ uint32_t half16(uint32_t w, int h) {
   return h ? (w >> 16) : (w & 0xffffu);
@@ -511,17 +534,18 @@ __global__ __launch_bounds__(64) void decode_combine_mfma(DecodeParams p) {
   for (int s0 = 0; s0 < ns; s0 += kChunk) {
     if (s0 > 0) load_chunk(s0, ns - 1);
     const int cnt = min(kChunk, ns - s0);
+    // Lane s < cnt holds split s0 + s; only lanes 0..15 take part.
     const float2 ml = lane < cnt ? ml_raw : make_float2(-INFINITY, 0.f);
-    const float m_new = fmaxf(M, wave_max(ml.x));
+    const float m_new = fmaxf(M, lane_value(row_max16(ml.x), 0));
     const float rescale = __builtin_amdgcn_exp2f(M - m_new);  // 0 on the first chunk
     const float f = __builtin_amdgcn_exp2f(ml.x - m_new);
-    den = den * rescale + wave_sum(f * ml.y);
+    den = den * rescale + lane_value(row_sum16(f * ml.y), 0);
     M = m_new;
 #pragma unroll
     for (int c = 0; c < C; ++c) num[c] *= rescale;
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
-      const float fj = __shfl(f, j);
+      const float fj = lane_value(f, j);
       // A select, not a product: rows past cnt may hold anything.
 #pragma unroll
       for (int c = 0; c < C; ++c) num[c] += j < cnt ? fj * a[j][c] : 0.f;
