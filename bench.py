@@ -98,6 +98,53 @@ def timed_graph(graph, replays, stream):
     return start.elapsed_time(stop) / 1e3  # seconds
 
 
+def sample_sclk(replay, seconds=1.5):
+    """Shader clock while `replay()` keeps the GPU busy: `amd-smi metric
+    --clock` polled from a second thread; the median, min and max over every
+    sample of every XCD's gfx clock (MHz), and the part's maximum. None when
+    amd-smi is absent or its output cannot be read."""
+    import shutil
+    import subprocess
+    import threading
+
+    import torch
+
+    tool = shutil.which("amd-smi") or "/opt/rocm/bin/amd-smi"
+    if not os.path.exists(tool):
+        return None
+    clocks, max_clk, stop = [], [], threading.Event()
+
+    def poll():
+        while not stop.is_set():
+            try:
+                res = subprocess.run([tool, "metric", "--clock", "--json"],
+                                     capture_output=True, text=True, timeout=10)
+                data = json.loads(res.stdout)
+                gpu = (data["gpu_data"] if isinstance(data, dict) else data)[0]
+                for name, clk in gpu["clock"].items():
+                    if name.startswith("gfx_"):
+                        clocks.append(float(clk["clk"]["value"]))
+                        max_clk.append(float(clk["max_clk"]["value"]))
+            except Exception:  # tool output not understood: report nothing
+                return
+
+    thread = threading.Thread(target=poll, daemon=True)
+    thread.start()
+    end = time.perf_counter() + seconds
+    while time.perf_counter() < end:
+        for _ in range(4):
+            replay()
+        torch.cuda.synchronize()
+    stop.set()
+    thread.join(timeout=15)
+    if not clocks:
+        return None
+    return {"median": statistics.median(clocks), "min": min(clocks), "max": max(clocks),
+            "part_max": max(max_clk), "samples": len(clocks),
+            "source": "amd-smi metric --clock (gfx clock of every XCD), polled while "
+                      "the workload's graph replays untimed"}
+
+
 def profile_run(args, device):
     """Eager, untimed launches of the benchmarked kernels (for rocprofv3)."""
     import torch
@@ -232,6 +279,7 @@ def bench_decode(args, device):
     t_step = timed_graph(graphs["step"], replays, stream)
     t_decode = timed_graph(graphs["decode"], replays, stream)
     steps = replays * LAYERS
+    sclk = sample_sclk(graphs["step"].replay)
     decode_bytes = wl.algorithmic_bytes()
     step_bytes = decode_bytes + wl.write_bytes()
     sec_per_step = t_step / steps
@@ -247,6 +295,7 @@ def bench_decode(args, device):
         "decode_bytes": decode_bytes,
         "step_bytes": step_bytes,
         "stream": stream,
+        "sclk": sclk,
     }
 
 
@@ -283,6 +332,8 @@ def bench_prefill(device, reps=4, calls_per_graph=10):
         g.replay()
         secs = timed_graph(g, reps, stream) / (reps * calls_per_graph)
         results[tile] = secs
+        if tile == 64:
+            sclk = sample_sclk(g.replay)
     best_tile = min(results, key=results.get)
     flops = wl.causal_flops()
     return {
@@ -292,6 +343,7 @@ def bench_prefill(device, reps=4, calls_per_graph=10):
         "best_tile": best_tile,
         "tflops": flops / results[best_tile] / 1e12,
         "wl": wl,
+        "sclk": sclk,
     }
 
 
@@ -641,6 +693,7 @@ def main():
             "step_bytes": dec["step_bytes"],
             "hbm_pct_of_peak": round(100 * dec["value_gbs"] / HBM_PEAK_GBS, 2),
             "decode_only_us": round(dec["decode_us"], 3),
+            "sclk_mhz": dec["sclk"],
         },
         "roofline": {
             "bound": "hbm",
@@ -668,6 +721,7 @@ def main():
                          "traffic": traffic["prefill_call_bytes"] if traffic else None},
             "flops_per_call": pre["flops_per_call"],
             "us_per_call_by_kv_tile": pre["us_per_call"],
+            "sclk_mhz_kv_tile_64": pre["sclk"],
             "cpu_baseline": cpu_pre,
         }
     if not args.no_pre_attention:
