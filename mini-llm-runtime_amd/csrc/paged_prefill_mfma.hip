@@ -46,6 +46,8 @@
 // not done here), and P is rounded to bf16 as the MFMA operand.
 #include "paged_prefill.h"
 
+#include <atomic>
+
 namespace mlr {
 namespace {
 
@@ -536,24 +538,25 @@ int launch(const PrefillParams &p, int64_t max_query_len, hipStream_t stream) {
   const int64_t blocks = static_cast<int64_t>(q.num_seqs) * q.n_qtiles * q.hq;
   if (blocks > INT32_MAX)
     return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_prefill: too many work items");
-  // CU count and workgroups per CU of this kernel, once per device.
+  // CU count and workgroups per CU of this kernel, queried once per device
+  // (threads that race here store the same values).
   constexpr int kMaxDevices = 64;
-  static int ncu_of[kMaxDevices], per_cu_of[kMaxDevices];
+  static std::atomic<int> ncu_of[kMaxDevices], per_cu_of[kMaxDevices];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return set_error(MLR_ERR_HIP, "mlr_paged_prefill: no current device");
-  if (ncu_of[dev] == 0) {
+  if (ncu_of[dev].load(std::memory_order_acquire) == 0) {
     int ncu = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu, reinterpret_cast<const void *>(prefill_mfma<D, BN, KS>), 256 * KS, 0) !=
             hipSuccess)
       return set_error(MLR_ERR_HIP, "mlr_paged_prefill: device query failed");
-    per_cu_of[dev] = per_cu;
-    ncu_of[dev] = ncu;
+    per_cu_of[dev].store(per_cu, std::memory_order_relaxed);
+    ncu_of[dev].store(ncu, std::memory_order_release);
   }
-  q.ncu = ncu_of[dev];
-  q.pair_cu = per_cu_of[dev] == 2 ? 1 : 0;
+  q.ncu = ncu_of[dev].load(std::memory_order_acquire);
+  q.pair_cu = per_cu_of[dev].load(std::memory_order_relaxed) == 2 ? 1 : 0;
   prefill_mfma<D, BN, KS><<<dim3(static_cast<unsigned>(blocks)), 256 * KS, 0, stream>>>(q);
   return check_launch("mlr_paged_prefill(mfma)");
 }
