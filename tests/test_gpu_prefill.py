@@ -188,6 +188,47 @@ def test_bf16_ragged_varlen_matches_oracle(device):
         assert max_abs(got[lo:hi], want) <= 2e-2, f"sequence {s}"
 
 
+@pytest.mark.parametrize("num_seqs", [40, 300])
+def test_bf16_many_sequences_match_oracle(device, num_seqs):
+    """Workgroups past twice the CU count (40 sequences: 1120 workgroups, the
+    rank pairing covers only the first 2 x CUs) and more work items than the
+    prologue ranks (300 sequences x 2 query tiles: the unranked order). Every
+    (sequence, head) must still be computed exactly once."""
+    hq, hkv, d, bs = 14, 2, 64, 16
+    gen = torch.Generator().manual_seed(num_seqs)
+    qlens = torch.randint(1, 201, (num_seqs,), generator=gen).tolist()
+    prefixes = torch.randint(0, 501, (num_seqs,), generator=gen).tolist()
+    ctxs = [p + c for p, c in zip(prefixes, qlens)]
+    nblk = [(c + bs - 1) // bs for c in ctxs]
+    total_blocks = sum(nblk) + 3
+    perm = torch.randperm(total_blocks, generator=gen).tolist()
+    tables, at = [], 0
+    for n in nblk:
+        tables.append(perm[at:at + n])
+        at += n
+    kc = torch.full((total_blocks, bs, hkv, d), float("nan"), dtype=torch.bfloat16)
+    vc = torch.full_like(kc, float("nan"))
+    qs = []
+    for s, ctx in enumerate(ctxs):
+        pos = torch.arange(ctx)
+        blocks = torch.tensor(tables[s])[pos // bs]
+        kc[blocks, pos % bs] = torch.randn(ctx, hkv, d, generator=gen).to(torch.bfloat16)
+        vc[blocks, pos % bs] = torch.randn(ctx, hkv, d, generator=gen).to(torch.bfloat16)
+        qs.append(torch.randn(qlens[s], hq, d, generator=gen).to(torch.bfloat16))
+    q = torch.cat(qs)
+    width = max(nblk)
+    bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.long)
+    qsl = torch.tensor([0] + list(itertools.accumulate(qlens)), dtype=torch.long)
+    got = kpa.paged_attention_prefill_varlen(
+        q.to(device), kc.to(device), vc.to(device), bt.to(device), qsl.to(device),
+        torch.tensor(ctxs, dtype=torch.long).to(device), bs, 64).cpu()
+    assert torch.isfinite(got).all()
+    for s in range(num_seqs):
+        lo, hi = int(qsl[s]), int(qsl[s + 1])
+        want = opa.prefill_chunk_tiled(q[lo:hi], kc, vc, tables[s], prefixes[s], ctxs[s], bs, 64)
+        assert max_abs(got[lo:hi], want) <= 2e-2, f"sequence {s}"
+
+
 @pytest.mark.parametrize("d,bs", [(64, 16), (128, 32), (40, 5)], ids=["d64", "d128", "generic"])
 def test_out_of_range_block_masks_its_tokens(device, d, bs):
     """An out-of-range block id in the table hides that block's keys."""
