@@ -647,9 +647,9 @@ def measured_traffic():
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the paged attention path has no cross-GPU "
-              "step in this build (see DESIGN.md, 'How the path would shard'); "
-              "run it with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: the paged attention kernels run one GPU's "
+              "share of the work and have no cross-GPU step; run it with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -91,8 +91,8 @@ def decode_batch_loop(q, k_cache, v_cache, block_tables, seq_lens, block_size):
 def decode_batch_parallel(q, k_cache, v_cache, block_tables, seq_lens, block_size):
     """Tensorized batched paged decode, q [B, Hq, D] -> [B, Hq, D].
 
-    Follows paged_attention.py:178-254, the north star's "tensorized PyTorch
-    paged path": physical ids block_tables[b, pos // bs] for every position up
+    Follows paged_attention.py:178-254, the reference's tensorized PyTorch
+    paged path: physical ids block_tables[b, pos // bs] for every position up
     to max(seq_lens) (:222-229), invalid positions pointed at block 0 (:230-232),
     a [B, maxS, Hkv, D] gather (:234-235), [B, Hq, maxS, D] after transpose and
     repeat_interleave (:238-240), scores = q @ k^T * scale in the input dtype
