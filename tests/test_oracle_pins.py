@@ -1,4 +1,4 @@
-"""Pin the oracle (CPU) before trusting it as the checker of the HIP kernels."""
+"""Pin the oracle (CPU) before trusting it as the reference for the HIP kernels."""
 
 from __future__ import annotations
 
