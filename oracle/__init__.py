@@ -4,8 +4,9 @@ This package restates, on the CPU with PyTorch/numpy, the algorithms of the
 reference (lv76/mini-llm-runtime) that the HIP library replaces. Each function
 cites the reference file:line it follows. Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import it, and only as the reference to compare against or the timed CPU baseline; the product
-package ``mini_llm_runtime_amd`` never imports it and never falls back to it.
+import it, and only as the reference to compare against or as the timed CPU
+baseline; the product package ``mini_llm_runtime_amd`` never imports it and
+never falls back to it.
 
 Modules
 - ``paged_attention``: decode (single request, per-request loop, tensorized
