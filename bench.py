@@ -79,6 +79,22 @@ def parse_args():
     return p.parse_args()
 
 
+def warm_graph(graph, stream, min_replays=1, seconds=0.25):
+    """Untimed replays of `graph`, at least `min_replays` and at least
+    `seconds` of them, so the timed region starts with the shader clock
+    already up; returns the number of replays."""
+    import torch
+    done = 0
+    end = time.perf_counter() + seconds
+    with torch.cuda.stream(stream):
+        while done < min_replays or time.perf_counter() < end:
+            for _ in range(4):
+                graph.replay()
+            done += 4
+            torch.cuda.synchronize()
+    return done
+
+
 def timed_graph(graph, replays, stream):
     """Seconds for `replays` graph launches, bracketed by events on `stream`.
 
@@ -272,11 +288,11 @@ def bench_decode(args, device):
 
     replays = max(1, -(-args.steps // LAYERS))
     warm = max(1, -(-args.warmup // LAYERS))
-    for _ in range(warm):
-        graphs["step"].replay()
-        graphs["decode"].replay()
-    torch.cuda.synchronize()
+    # At least the requested warm-up, and at least 0.25 s of it, before each
+    # timed region (the clock ramps under sustained load).
+    warm = warm_graph(graphs["step"], stream, warm)
     t_step = timed_graph(graphs["step"], replays, stream)
+    warm_graph(graphs["decode"], stream, warm)
     t_decode = timed_graph(graphs["decode"], replays, stream)
     steps = replays * LAYERS
     sclk = sample_sclk(graphs["step"].replay)
@@ -329,7 +345,7 @@ def bench_prefill(device, reps=4, calls_per_graph=10):
         with torch.cuda.graph(g, stream=stream):
             for _ in range(calls_per_graph):
                 call()
-        g.replay()
+        warm_graph(g, stream)
         secs = timed_graph(g, reps, stream) / (reps * calls_per_graph)
         results[tile] = secs
         if tile == 64:
@@ -380,7 +396,7 @@ def bench_pre_attention(device, reps=4, calls_per_graph=10):
         with torch.cuda.graph(g, stream=stream):
             for _ in range(calls_per_graph):
                 fn()
-        g.replay()
+        warm_graph(g, stream, seconds=0.1)
         return timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
 
     out = {}
@@ -461,7 +477,7 @@ def bench_decode_32k(device, reps=4, calls_per_graph=5):
         with torch.cuda.graph(g, stream=stream):
             for _ in range(calls_per_graph):
                 step()
-        g.replay()
+        warm_graph(g, stream)
         us = timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
         sweep["default" if splits == 0 else str(splits)] = round(us, 2)
     best = min(sweep, key=sweep.get)
@@ -491,7 +507,7 @@ def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=10):
     with torch.cuda.graph(g, stream=stream):
         for _ in range(calls_per_graph):
             paged_attention_accumulator_cuda(p, v)
-    g.replay()
+    warm_graph(g, stream)
     us = timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
     nbytes = batch * (64 * 256 + 64 + 256) * 4
     return {"workload": f"accumulator_b{batch}_n64_d256_fp32", "us": round(us, 3),
