@@ -303,8 +303,20 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   for (int j = 0; j < QK; ++j)
     qraw[j] = head_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * j + 8 * g)
                       : make_uint4(0, 0, 0, 0);
+  // Token positions fit in 32 bits here (max_blocks * block_size < 2^31;
+  // speculative tile positions stay below 2^32): block index and offset by
+  // shift and mask when block_size is a power of two, else 32-bit division.
+  const uint32_t bs32 = static_cast<uint32_t>(p.block_size);
+  const bool bs_pow2 = (bs32 & (bs32 - 1)) == 0;
+  const uint32_t bs_shift = static_cast<uint32_t>(__builtin_ctz(bs32));
+  auto block_of = [&](uint32_t pos) -> uint32_t {
+    return bs_pow2 ? (pos >> bs_shift) : pos / bs32;
+  };
+  auto in_block = [&](uint32_t pos) -> uint32_t {
+    return bs_pow2 ? (pos & (bs32 - 1)) : pos % bs32;
+  };
   auto raw_block_id = [&](int k) -> int64_t {
-    const int64_t idx = (t0 + 16LL * (w + kWaves * k)) / p.block_size;
+    const int64_t idx = block_of(static_cast<uint32_t>(t0) + 16u * (w + kWaves * k));
     return idx < p.max_blocks ? bt_row[idx] : int64_t(-1);
   };
   int64_t blk_raw = raw_block_id(lane);
@@ -389,7 +401,8 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   // new slot is the one position ctx - 1 maps to.
   auto mark_new_row = [&](Tile<D> &t) {
     const bool same_slot =
-        t.blk >= 0 && new_slot == (int64_t)t.blk * p.block_size + last_pos % p.block_size;
+        t.blk >= 0 &&
+        new_slot == (int64_t)t.blk * p.block_size + in_block(static_cast<uint32_t>(last_pos));
     if (same_slot) t.sub = last_tok;
   };
 
@@ -401,7 +414,8 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
       const int blk = k < nk ? __builtin_amdgcn_readlane(blk_reg, k & 63) : -1;
       const int rel = 16 * (w + kWaves * k);
       // Byte offset of the tile's first token inside its block.
-      const int tile_off = static_cast<int>((t0 + rel) % p.block_size) * row_elems * 2;
+      const int tile_off =
+          static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel)) * row_elems * 2;
       load_tile<D>(buf[u], kc, vc, block_elems, tile_off, blk, rel, lo);
     }
     if (append_here) {
@@ -423,17 +437,17 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   // barrier, with or without tiles).
   if constexpr (kDouble) {
     // Next batch in flight while the current one computes.
+    // Batches are issued whether or not they hold tiles (absent tiles read
+    // zeros), so the wait before each compute counts only its own batch.
     Tile<D> bufA[kBatch], bufB[kBatch];
-    if (nk > 0) issue(bufA, 0);
+    issue(bufA, 0);
     if (append_here) stage_new_row();
-    if (nk > 0) {
-      for (int kb = 0; kb < nk; kb += 2 * kBatch) {
-        if (kb + kBatch < nk) issue(bufB, kb + kBatch);
-        compute(bufA);
-        if (kb + kBatch >= nk) break;
-        if (kb + 2 * kBatch < nk) issue(bufA, kb + 2 * kBatch);
-        compute(bufB);
-      }
+    for (int kb = 0; kb < nk; kb += 2 * kBatch) {
+      issue(bufB, kb + kBatch);
+      compute(bufA);
+      if (kb + kBatch >= nk) break;
+      issue(bufA, kb + 2 * kBatch);
+      compute(bufB);
     }
   } else {
     // Issued whatever nk is (absent tiles read zeros), so that every path
