@@ -110,11 +110,6 @@ __device__ __forceinline__ float lane_value(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
-// 16-bit half `h` (0 = low, 1 = high) of word w.
-__device__ __forceinline__ uint32_t half16(uint32_t w, int h) {
-  return h ? (w >> 16) : (w & 0xffffu);
-}
-
 template <int D>
 __device__ __forceinline__ uint32_t vword(const typename VRow<D>::type &v, int c) {
   if constexpr (D == 64) {
@@ -262,8 +257,10 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
 #pragma unroll
   for (int n = 0; n < VC; ++n) {
     const int c = n >> 1, h = n & 1;
-    const uint32_t lo = half16(vword<D>(t.v[0], c), h) | (half16(vword<D>(t.v[1], c), h) << 16);
-    const uint32_t hi = half16(vword<D>(t.v[2], c), h) | (half16(vword<D>(t.v[3], c), h) << 16);
+    // Half h of the words of rows 0/1 (and 2/3), one v_perm_b32 each.
+    const uint32_t sel = h ? 0x07060302u : 0x05040100u;
+    const uint32_t lo = __builtin_amdgcn_perm(vword<D>(t.v[1], c), vword<D>(t.v[0], c), sel);
+    const uint32_t hi = __builtin_amdgcn_perm(vword<D>(t.v[3], c), vword<D>(t.v[2], c), sel);
     const s16x4_t va = __builtin_bit_cast(s16x4_t, make_uint2(lo, hi));
     st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, st.acc[n], 0, 0, 0);
   }
