@@ -48,10 +48,14 @@ template <int D> struct VRow;
 template <> struct VRow<64> { using type = uint2; };   // 4 bf16 per lane
 template <> struct VRow<128> { using type = uint4; };  // 8 bf16 per lane
 
-__device__ __forceinline__ float bf16_round(float x) {
-  // v_cvt_pk_bf16_f32 rounds to nearest even.
-  const __bf16 h = static_cast<__bf16>(x);
-  return static_cast<float>(h);
+// a and b rounded to bf16 (nearest even) and back to FP32, with one
+// v_cvt_pk_bf16_f32 for the pair.
+__device__ __forceinline__ void bf16_round2(float &a, float &b) {
+  typedef float f32x2_v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{a, b}, bf16x2_v));
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
 }
 
 __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
@@ -227,12 +231,16 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
   for (int j = 0; j < QK; ++j)
     s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, t.k[j]),
                                                 qf[j], s, 0, 0, 0);
+  float r[4] = {s[0], s[1], s[2], s[3]};
+  bf16_round2(r[0], r[1]);
+  bf16_round2(r[2], r[3]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] *= scale;
+  bf16_round2(r[0], r[1]);
+  bf16_round2(r[2], r[3]);
   float x[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float r = bf16_round(bf16_round(s[i]) * scale);
-    x[i] = (4 * g + i < lim) ? r * kLog2e : -INFINITY;
-  }
+  for (int i = 0; i < 4; ++i) x[i] = (4 * g + i < lim) ? r[i] * kLog2e : -INFINITY;
   float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
   mx = max_xor32(max_xor16(mx));
   const float m_new = fmaxf(st.m, mx);  // finite: every tile has a live token
