@@ -341,9 +341,13 @@ class TinyQwen2Model(nn.Module):
         bs, width = kv_cache.block_size, block_tables.shape[1]
         device = position_ids.device
         lens = query_start_loc[1:] - query_start_loc[:-1]
-        owner = torch.repeat_interleave(
-            torch.arange(context_lens.shape[0], device=device), lens.clamp(min=0),
-            output_size=num_tokens)
+        # Request of each packed row: how many request ends lie at or before
+        # it. A binary search stays in bounds whatever query_start_loc holds,
+        # so a malformed one reaches its own check below instead of a
+        # size mismatch inside a device kernel.
+        owner = torch.searchsorted(
+            query_start_loc[1:].contiguous(), torch.arange(num_tokens, device=device),
+            right=True).clamp_(max=context_lens.shape[0] - 1)
         first = (context_lens - lens)[owner]
         offset = torch.arange(num_tokens, device=device) - query_start_loc[:-1][owner]
         required = (context_lens + bs - 1) // bs

@@ -489,8 +489,12 @@ class Qwen2Attention(nn.Module):
         expected_slots = table_t[positions // bs] * bs + positions % bs
         if not torch.equal(slot_mapping.to(torch.long), expected_slots):
             raise ValueError("slot_mapping does not match block_table for the chunk positions")
-        # Slots are distinct and in range: they follow a validated table.
         self._check_fused_inputs(hidden_states, position_ids, kv_cache, slot_mapping)
+        # write_slots' value checks (reference runtime/paged_kv_cache.py:235-239,
+        # reached from model/qwen2.py:741-746): a table that repeats a block
+        # inside the chunk's range passes the checks above but maps two
+        # positions to one slot.
+        kv_cache.check_slots(slot_mapping)
         query = self._fused_qkv_rope_write(hidden_states[0], position_ids[0], kv_cache,
                                            layer_idx, slot_mapping)
         k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)

@@ -193,14 +193,87 @@ def qwen7b_32k():
     return workloads.bf16_decode_qwen7b_32k()
 
 
+def _textbook_rows(q, kc, vc, table, length, bs):
+    """float64 attention of every query head of one sequence, [Hq, D]."""
+    hq, d = q.shape
+    hkv = kc.shape[2]
+    group = hq // hkv
+    pos = torch.arange(length)
+    blocks = torch.tensor(table)[pos // bs]
+    k = kc[blocks, pos % bs].double()            # [S, Hkv, D]
+    v = vc[blocks, pos % bs].double()
+    qg = q.double().view(hkv, group, d)          # query head h reads KV head h // group
+    logits = torch.einsum("skd,kgd->kgs", k, qg) / math.sqrt(d)
+    w = torch.softmax(logits, dim=-1)
+    return torch.einsum("kgs,skd->kgd", w, v).reshape(hq, d)
+
+
+@pytest.fixture(scope="module")
+def qwen7b_32k_textbook(qwen7b_32k):
+    wl = qwen7b_32k
+    return torch.stack([_textbook_rows(wl.q[b], wl.k_cache, wl.v_cache, wl.tables[b],
+                                       int(wl.context_lens[b]), 16)
+                        for b in range(wl.q.shape[0])])
+
+
+def test_textbook_rows_match_the_row_form(qwen7b_32k, qwen7b_32k_textbook):
+    """The vectorised float64 reference equals the one-row form on a few rows."""
+    wl = qwen7b_32k
+    for b, h in ((0, 0), (3, 13), (7, 27)):
+        one = _textbook_row(wl.q[b, h], wl.k_cache, wl.v_cache, wl.tables[b], 32768, h // 7, 16)
+        assert np.abs(qwen7b_32k_textbook[b, h].numpy() - one).max() <= 1e-12
+
+
 @pytest.mark.parametrize("splits", [4, 8, 16, 32])
-def test_qwen7b_32k_split_sweep(device, qwen7b_32k, splits):
-    """BF16 decode at Qwen2.5-7B shape, context 32768, split count swept."""
+def test_qwen7b_32k_split_sweep(device, qwen7b_32k, qwen7b_32k_textbook, splits):
+    """BF16 decode at Qwen2.5-7B shape, context 32768, split count swept;
+    every (sequence, query head) row against float64 attention."""
     wl = qwen7b_32k
     ts = math.ceil(32768 / splits / 16) * 16
     got = run_decode(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, 16,
-                     device, tokens_per_split=ts).float().cpu()
-    for b, h in ((0, 0), (3, 13), (7, 27)):
-        want = _textbook_row(wl.q[b, h], wl.k_cache, wl.v_cache, wl.tables[b], 32768,
-                             h // 7, 16)
-        assert np.abs(got[b, h].numpy() - want).max() <= 2e-2
+                     device, tokens_per_split=ts).double().cpu()
+    err = (got - qwen7b_32k_textbook).abs()
+    print(f"qwen7b_32k splits {splits}: max-abs over {err.shape[0] * err.shape[1]} rows "
+          f"{err.max().item():.3e}")
+    assert err.max().item() <= 2e-2
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,seq_lens,tables",
+    [
+        (4, 2, [3, 5], [[2, 0, -1], [1, 3, 4]]),
+        (2, 2, [3, 5], [[2, 0, -1], [1, 3, 4]]),
+        (4, 1, [3, 5], [[2, 0, -1], [1, 3, 4]]),
+        (4, 2, [3, 4], [[2, 0], [1, 3]]),
+    ],
+    ids=["gqa-ragged", "mha-ragged", "mqa-ragged", "seq-length-equals-heads"],
+)
+def test_per_request_loop_matches_oracle_loop(device, hq, hkv, seq_lens, tables):
+    """paged_attention_decode_batch_reference (the per-request loop, reference
+    kernels/reference/paged_attention.py:109-176) against the oracle's loop,
+    and equal to the batched decode (tests/kernels/test_paged_attention_batch.py:
+    10-43 of the reference)."""
+    torch.manual_seed(42)
+    q = torch.randn(len(seq_lens), hq, 8)
+    kc = torch.randn(5, 2, hkv, 8)
+    vc = torch.randn_like(kc)
+    want = opa.decode_batch_loop(q, kc, vc, tables, seq_lens, 2)
+    got = kpa.paged_attention_decode_batch_reference(
+        q.to(device), kc.to(device), vc.to(device), tables, seq_lens, 2)
+    assert got.shape == q.shape and got.device.type == "cuda"
+    assert max_abs(got, want) <= 1e-5
+    batched = run_decode(q, kc, vc, torch.tensor(tables), torch.tensor(seq_lens), 2, device)
+    assert max_abs(got, batched) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_per_request_loop_qwen05b_shape(device, dtype):
+    """The per-request loop at Qwen2.5-0.5B head shape on ragged contexts,
+    against the oracle loop (1e-5 FP32, 2e-2 BF16)."""
+    lens = [1, 17, 300, 1000]
+    q, kc, vc, _, _, tables = random_paged(lens, 14, 2, 64, 16, dtype=dtype, seed=31)
+    want = opa.decode_batch_loop(q, kc, vc, tables, lens, 16)
+    got = kpa.paged_attention_decode_batch_reference(
+        q.to(device), kc.to(device), vc.to(device), tables, lens, 16)
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) <= TOL[dtype]

@@ -239,3 +239,65 @@ def test_decode_steps_follow_the_prefill(device):
         rows.append(module_rows(module, x, pos, device))
     check_caches(dev, ora, written, torch.cat([r[0] for r in rows]),
                  torch.cat([r[1] for r in rows]))
+
+
+def _device_decode_case(device, dtype=torch.float32):
+    """The reference's make_decode_case (tests/model/test_qwen2_batch_decode.py:
+    15-31): two decode requests over a 6-block, block-size-2 pool of layer 1,
+    here on the device."""
+    cfg = types.SimpleNamespace(hidden_size=64, num_attention_heads=4, num_key_value_heads=2,
+                                head_dim=16, rope_theta=1_000_000.0)
+    torch.manual_seed(42)
+    module = Qwen2Attention(cfg).to(dtype=dtype).to(device)
+    cache = PagedKVCache(2, 6, 2, 2, 16, dtype=dtype, device=device)
+    cache.k_cache.normal_()
+    cache.v_cache.normal_()
+    inputs = dict(
+        hidden_states=torch.randn(2, 1, 64, dtype=dtype, device=device),
+        position_ids=torch.tensor([[2], [4]], device=device),
+        layer_idx=1,
+        slot_mapping=torch.tensor([0, 8], device=device),
+        block_tables=torch.tensor([[2, 0, -1], [1, 3, 4]], device=device),
+        context_lens=torch.tensor([3, 5], device=device),
+    )
+    return module, cache, inputs
+
+
+@pytest.mark.parametrize("field,value,message", [
+    ("hidden_states", torch.zeros(2, 2, 64), "hidden_states must have shape"),
+    ("position_ids", torch.tensor([[1], [4]]), "decode positions"),
+    ("context_lens", torch.tensor([0, 5]), "greater than 0"),
+    ("block_tables", torch.tensor([[2, 0], [1, 3]]), "insufficient blocks"),
+    ("block_tables", torch.tensor([[2, -1, -1], [1, 3, 4]]), "invalid physical block"),
+    ("slot_mapping", torch.tensor([1, 8]), "slot_mapping must match"),
+    ("slot_mapping", torch.tensor([8, 8]), "slot_mapping must match"),
+    ("context_lens", torch.tensor([3., 5.]), "torch.long dtype"),
+])
+def test_device_batch_decode_rejects_metadata_before_cache_write(device, field, value,
+                                                                 message):
+    """Reference tests/model/test_qwen2_batch_decode.py:74-94 on a device
+    cache: the metadata checks run on the device (one reduction, one host
+    sync) before the fused write and the decode launch, so a rejected call
+    leaves both layers of the cache bit-identical."""
+    module, cache, inputs = _device_decode_case(device)
+    old_k, old_v = cache.k_cache.clone(), cache.v_cache.clone()
+    inputs[field] = value.to(device)
+    with pytest.raises(ValueError, match=message):
+        with torch.no_grad():
+            module.forward_decode_batch_with_cache(kv_cache=cache, **inputs)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k_cache, old_k)
+    assert torch.equal(cache.v_cache, old_v)
+
+
+def test_device_batch_decode_accepts_the_unmutated_case(device):
+    """The same case without a mutation runs and writes exactly the two slots
+    of layer 1 (the other slots and layer 0 keep their bits)."""
+    module, cache, inputs = _device_decode_case(device)
+    old_k = cache.k_cache.clone()
+    with torch.no_grad():
+        out = module.forward_decode_batch_with_cache(kv_cache=cache, **inputs)
+    assert out.shape == (2, 1, 64) and torch.isfinite(out).all()
+    changed = (cache.k_cache != old_k).reshape(2, 12, -1).any(-1).cpu()
+    assert not changed[0].any()
+    assert changed[1].nonzero().flatten().tolist() == [0, 8]

@@ -53,9 +53,13 @@ def make_model(cfg_kwargs, dtype, device, seed=0):
     return cfg, model.to(device=device, dtype=dtype).eval(), oracle
 
 
-def check_tokens(request_id, got, want, margins):
-    """got == want, up to a near-tie step (see module). Returns the step of a
-    near-tie divergence, or None."""
+def check_tokens(request_id, got, want, margins, exemptions=None, branches=None):
+    """got == want, up to a near-tie step (see module). At a near tie where
+    the run took the oracle's second choice, the comparison continues along
+    the oracle's branch for that choice when `branches` holds it (the golden
+    files do), else stops there. Returns the number of tokens compared. Each
+    exemption is printed, and appended to `exemptions` as (request_id, step,
+    margin, tokens left uncompared)."""
     assert len(got) == len(want), (request_id, got, want)
     for i, (g, w) in enumerate(zip(got, want)):
         if g == w:
@@ -64,8 +68,25 @@ def check_tokens(request_id, got, want, margins):
         assert margin < NEAR_TIE and g == second, (
             f"request {request_id} step {i}: got {g}, oracle {w} "
             f"(margin {margin:.3g}, second {second})")
-        return i  # diverged at a near tie: the rest follows another context
-    return None
+        branch = next((b for b in branches or () if b["step"] == i), None)
+        if branch is not None:
+            rest = got[i:]
+            sub = check_tokens(f"{request_id}/branch{i}", rest, branch["tokens"][:len(rest)],
+                               list(zip(branch["margins"], branch["second"]))[:len(rest)],
+                               exemptions)
+            left = len(rest) - sub
+            print(f"near-tie exemption: request {request_id} step {i}, oracle margin "
+                  f"{margin:.3g}, took the oracle's second choice {g}; compared along the "
+                  f"oracle's branch for it, {left} tokens not compared")
+        else:
+            sub, left = 0, len(got) - i
+            print(f"near-tie exemption: request {request_id} step {i}, oracle margin "
+                  f"{margin:.3g}, took the oracle's second choice {g}; {left} tokens from "
+                  f"this step on not compared")
+        if exemptions is not None:
+            exemptions.append((request_id, i, margin, left))
+        return i + sub
+    return len(got)
 
 
 def random_prompt(gen, vocab, length):
@@ -232,7 +253,12 @@ def test_qwen05b_serving_fp32_matches_oracle_tokens(device):
         for _ in range(w.steps):
             run_generation_step(model, scheduler)
     by_id = {r.request_id: r for r in requests}
-    compared = 0
+    # The golden's own near ties: the only (request, step) pairs where a run
+    # may take the oracle's second choice.
+    near_ties = {(g["request_id"], i) for g in golden["requests"]
+                 for i, m in enumerate(g["margins"]) if m < NEAR_TIE}
+    print(f"golden near ties (margin < {NEAR_TIE}): {sorted(near_ties)}")
+    compared, exemptions = 0, []
     for g in golden["requests"]:
         r = by_id[g["request_id"]]
         assert r.prompt_len == g["prompt_len"]
@@ -240,6 +266,11 @@ def test_qwen05b_serving_fp32_matches_oracle_tokens(device):
         assert got, f"{r.request_id} never ran"
         margins = list(zip(g["margins"], g["second"]))
         want = g["tokens"][:len(got)]
-        stopped = check_tokens(r.request_id, got, want, margins)
-        compared += len(got) if stopped is None else stopped
+        compared += check_tokens(r.request_id, got, want, margins, exemptions,
+                                 g.get("branches"))
+    top = [(rid, step) for rid, step, _, _ in exemptions if "/" not in rid]
+    assert set(top) <= near_ties
+    uncompared = sum(left for rid, *_, left in exemptions if "/" not in rid)
+    print(f"serving fp32: {compared} tokens identical to the oracle's, "
+          f"{len(exemptions)} near-tie exemption(s), {uncompared} tokens not compared")
     assert compared >= 200

@@ -220,6 +220,59 @@ def test_qwen2_chunk_prefill_validation_messages(kwargs, message):
             kwargs["prefix_len"], kwargs["context_len"], kwargs.get("tile_size", 4))
 
 
+def test_qwen2_chunk_prefill_rejects_repeated_block_before_writing():
+    """A table that repeats a block inside the chunk's range passes the
+    table/slot checks (every slot follows the table) but maps two positions to
+    one slot; write_slots rejects that (reference paged_kv_cache.py:238-239,
+    reached from model/qwen2.py:741-746) before anything is written."""
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+    attn, cfg = _tiny_attention()
+    cache = PagedKVCache(1, 8, 4, 2, 8, dtype=torch.float32)
+    cache.k_cache.fill_(3)
+    before = cache.k_cache.clone()
+    slots = torch.tensor([12, 13, 14, 15, 12, 13, 14, 15])
+    with pytest.raises(ValueError, match="slot_mapping must contain distinct slots"):
+        attn.forward_prefill_chunk_with_cache(
+            torch.zeros(1, 8, cfg.hidden_size), torch.arange(8).unsqueeze(0), cache, 0,
+            slots, [3, 3], 0, 8, 4)
+    assert torch.equal(cache.k_cache, before)
+
+
+def _tiny_model():
+    from mini_llm_runtime_amd.model.qwen2 import TinyQwen2Config, TinyQwen2Model
+    cfg = TinyQwen2Config(vocab_size=32, hidden_size=32, intermediate_size=64,
+                          num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2)
+    torch.manual_seed(0)
+    return TinyQwen2Model(cfg), cfg
+
+
+@pytest.mark.parametrize("qsl,message", [
+    ([1, 3], "query_start_loc must start at 0"),
+    ([0, 2], "query_start_loc must end at the packed token count"),
+    ([0, 4], "query_start_loc must end at the packed token count"),
+    ([0, 0, 3], "query_start_loc must be strictly increasing"),
+    ([0, 3, 2], "query_start_loc must be strictly increasing"),
+])
+def test_packed_prefill_rejects_bad_query_start_loc(qsl, message):
+    """Each malformed query_start_loc raises its own message (no size error
+    from building the token-to-request map first), and nothing is written."""
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+    model, cfg = _tiny_model()
+    cache = PagedKVCache(1, 8, 4, 2, 8, dtype=torch.float32)
+    cache.k_cache.fill_(9)
+    before = cache.k_cache.clone()
+    requests = len(qsl) - 1
+    ids = torch.tensor([1, 2, 3])
+    positions = torch.tensor([0, 1, 2])
+    slots = torch.tensor([4, 5, 6])
+    tables = torch.tensor([[1, 2]] * requests)
+    ctx = torch.tensor([3] * requests)
+    with pytest.raises(ValueError, match=message):
+        model.forward_prefill_packed_with_cache(ids, positions, cache, slots, tables,
+                                                torch.tensor(qsl), ctx, 3)
+    assert torch.equal(cache.k_cache, before)
+
+
 def test_qwen2_attention_matches_reference_state_dict_names():
     attn, _ = _tiny_attention()
     assert list(attn.state_dict()) == [
