@@ -178,7 +178,7 @@ def profile_run(args, device):
     q, bt, ctx = wl.q.to(device), wl.block_tables.to(device), wl.context_lens.to(device)
     slots, new_k, new_v = (t.to(device) for t in (wl.slot_mapping, wl.new_k, wl.new_v))
     out = torch.empty_like(q)
-    ws = torch.empty(kpa.decode_workspace_bytes(64, 14, 64, bt.shape[1] * 16, torch.bfloat16),
+    ws = torch.zeros(kpa.decode_workspace_bytes(64, 14, 64, bt.shape[1] * 16, torch.bfloat16),
                      dtype=torch.uint8, device=device)
     for i in range(args.steps):
         k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
@@ -255,7 +255,7 @@ def bench_decode(args, device):
     out = torch.empty_like(q)
     ts = args.tokens_per_split
     ws_bytes = kpa.decode_workspace_bytes(64, 14, 64, bt.shape[1] * 16, torch.bfloat16, ts)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)
 
     def step(layer, with_write=True):
         # The decode step's KV write is folded into the decode call
@@ -460,7 +460,7 @@ def bench_decode_32k(device, reps=4, calls_per_graph=5):
     sweep = {}
     for splits in SPLITS_32K:
         ts = 0 if splits == 0 else 32768 // splits
-        ws = torch.empty(kpa.decode_workspace_bytes(8, 28, 128, bt.shape[1] * 16,
+        ws = torch.zeros(kpa.decode_workspace_bytes(8, 28, 128, bt.shape[1] * 16,
                                                     torch.bfloat16, ts),
                          dtype=torch.uint8, device=device)
 

@@ -4,7 +4,8 @@
  * The library implements the three kernels of the paged attention path of
  * mini-llm-runtime on gfx950 (MI355X):
  *   1. the KV-cache write: a slot_mapping scatter into one layer's block pool;
- *   2. batched single-token paged decode (split-KV, two passes);
+ *   2. batched single-token paged decode (split-KV; the splits merge in the
+ *      same launch on the bf16 matrix-core path, in a second one otherwise);
  *   3. paged chunk-prefill attention (causal by absolute token position).
  *
  * Conventions shared by every entry point:
@@ -111,7 +112,14 @@ size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
  *                  block_table_stride; entries past ceil(ctx/block_size) unused
  *   context_lens : int64 [batch]; each in [1, max_blocks_per_seq * block_size]
  *   tokens_per_split: split-KV granularity in tokens (<= 0: library default)
- *   workspace    : >= mlr_paged_decode_workspace_size(...) bytes, 256-aligned
+ *   workspace    : >= mlr_paged_decode_workspace_size(...) bytes, 256-aligned,
+ *                  all-zero before its first use (hipMemset once). It holds
+ *                  per-(sequence, KV head) arrival counters that the bf16
+ *                  matrix-core kernel uses to merge the splits in one launch
+ *                  (the last split of a sequence to finish merges them); every
+ *                  call returns them to zero, so the workspace can be reused
+ *                  without clearing, including inside captured graphs. Calls
+ *                  that share a workspace must not overlap.
  *   out          : [batch, num_q_heads, head_dim], strides (out_stride_b, out_stride_h)
  */
 int mlr_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,

@@ -25,6 +25,7 @@ struct DecodeParams {
   double scale;
   int ts;          // tokens per split
   int max_splits;  // splits covering max_blocks * block_size tokens
+  int *ws_ctr;     // [batch][hkv] arrival counters of the single-launch merge
   float2 *ws_ml;   // [batch][hq][max_splits] = (m, l)
   void *ws_acc;    // [batch][hq][max_splits][d], FP32 (FP64 for f64 inputs)
   int ml_base2;    // 1: m is a base-2 exponent, 0: natural-log units
@@ -39,13 +40,19 @@ struct DecodeParams {
   void *vc_w;
 };
 
+// Workspace: arrival counters (zero between calls), then the split partials
+// (m, l) and acc, each part 256-byte aligned.
 struct DecodeWorkspace {
-  int64_t ml_bytes;
+  int64_t ml_offset;
   int64_t acc_offset;
   int64_t total;
 };
 
-int64_t default_tokens_per_split(bool mfma, int64_t max_context);
+// Tokens per split of the head_dim-64 matrix-core kernel whose waves land a
+// fifth tile in LDS.
+constexpr int kLdsSplit64 = 320;
+
+int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_context);
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype);
 

@@ -215,14 +215,17 @@ int launch_combine(const DecodeParams &p, hipStream_t stream) {
 
 template int launch_combine<bf16_t>(const DecodeParams &, hipStream_t);
 
-int64_t default_tokens_per_split(bool mfma, int64_t max_context) {
+int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_context) {
   // Generic kernel: 256 tokens, whose scores it holds in LDS. Matrix-core
-  // kernel: at least 256 tokens (16 tiles, four per wave, loaded in one
-  // batch), and at most 16 splits per sequence: long contexts then get fewer,
-  // longer splits (measured at 8 x 32K tokens: 133 us with 128 splits,
-  // 108-111 us with 8-16), and the combine merges every sequence in one
-  // 16-split chunk.
+  // kernel at head_dim 64 with contexts of up to 16 x 320 tokens: 320 (four
+  // tiles per wave in registers and one in LDS), so a batch of long contexts
+  // fits the GPU in one generation of workgroups. Otherwise at least 256
+  // tokens (16 tiles, four per wave, loaded in one batch), and at most 16
+  // splits per sequence: long contexts then get fewer, longer splits
+  // (measured at 8 x 32K tokens: 133 us with 128 splits, 108-111 us with
+  // 8-16), and the merge takes every sequence in one 16-split chunk.
   if (!mfma) return 256;
+  if (head_dim == 64 && max_context <= 16 * kLdsSplit64) return kLdsSplit64;
   const int64_t per16 = ceil_div(max_context, 16);
   return per16 <= 256 ? 256 : ceil_div(per16, 256) * 256;
 }
@@ -230,9 +233,12 @@ int64_t default_tokens_per_split(bool mfma, int64_t max_context) {
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype) {
   DecodeWorkspace w;
+  // One arrival counter per (sequence, KV head); hq bounds the KV head count.
+  const int64_t ctr_bytes = batch * hq * static_cast<int64_t>(sizeof(int));
+  w.ml_offset = (ctr_bytes + 255) / 256 * 256;
   const int64_t rows = batch * hq * max_splits;
-  w.ml_bytes = rows * static_cast<int64_t>(sizeof(float2));
-  w.acc_offset = (w.ml_bytes + 255) / 256 * 256;
+  const int64_t ml_bytes = rows * static_cast<int64_t>(sizeof(float2));
+  w.acc_offset = w.ml_offset + (ml_bytes + 255) / 256 * 256;
   const int64_t acc_elem = dtype == MLR_DTYPE_F64 ? 8 : 4;
   w.total = w.acc_offset + rows * d * acc_elem;
   return w;
@@ -308,7 +314,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
       aligned && max_context < (int64_t(1) << 31) &&
       decode_mfma_eligible(dtype, head_dim, num_q_heads / num_kv_heads, block_size);
   int64_t ts = tokens_per_split > 0 ? tokens_per_split
-                                    : default_tokens_per_split(mfma, max_context);
+                                    : default_tokens_per_split(mfma, head_dim, max_context);
   if (!mfma) {
     MLR_REQUIRE(ts <= kGenMaxSplit,
                 "mlr_paged_decode: tokens_per_split %lld exceeds %d for this "
@@ -354,7 +360,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
   p.scale = scale;
   p.ts = static_cast<int>(ts);
   p.max_splits = static_cast<int>(max_splits);
-  p.ws_ml = static_cast<float2 *>(workspace);
+  p.ws_ctr = static_cast<int *>(workspace);
+  p.ws_ml = reinterpret_cast<float2 *>(static_cast<unsigned char *>(workspace) + wl.ml_offset);
   p.ws_acc = static_cast<unsigned char *>(workspace) + wl.acc_offset;
   p.ml_base2 = mfma ? 1 : 0;
   p.out = out;

@@ -1,6 +1,11 @@
-// bf16 split-KV paged decode on gfx950 matrix cores.
+// bf16 split-KV paged decode on gfx950 matrix cores, in one launch.
 //
-// One workgroup of four wavefronts per (sequence, KV head, split). The split's
+// One workgroup of four wavefronts per (live split, KV head). A split is
+// tokens_per_split tokens of one sequence; the live splits of all sequences
+// are numbered sequence by sequence and every workgroup finds its own from a
+// prefix sum of the context lengths, so no workgroup is spent on a split past
+// a sequence's end (only the grid's tail, sized for the widest table, exits
+// at once). The split's
 // 16-token tiles are dealt round-robin to the four waves; each wave keeps the
 // online-softmax state of all (<= 16) query heads of the KV head's GQA group,
 // so every K/V byte is read from HBM exactly once for the whole group.
@@ -25,9 +30,14 @@
 // current one (two register buffers), so 8-16 KiB per wave are in flight.
 //
 // The four waves merge through LDS. A sequence that fits one split writes its
-// output directly; otherwise each workgroup stores its split's (m, l, acc) and
-// the combine kernel merges the splits of each (sequence, KV head):
+// output directly; otherwise each workgroup stores its split's (m, l, acc)
+// with device-coherent stores and bumps the (sequence, KV head) counter, and
+// the workgroup that arrives last merges every split of the group:
 //   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s.
+// That saves the second launch of a separate combine kernel (about 1.9 us of
+// launch gap plus a memory round trip per step); the counters and partials
+// go through memory, not an XCD's L2, so the merge holds wherever the
+// hardware places the workgroups.
 //
 // Scores are rounded like the reference's bf16 matmul (to bf16, times scale,
 // to bf16 again: kernels/reference/paged_attention.py:246-247) before the
@@ -200,6 +210,56 @@ __device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
   }
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// A tile landed in LDS instead of registers (head_dim 64): 16 rows of one KV
+// head, K (2 KB) then V (2 KB), copied straight from memory by
+// buffer_load_dwordx4 ... lds (lane l of copy i writes LDS bytes
+// 1024 i + 16 l). Row r's 16-byte chunk c lands at chunk c ^ (r & 7), which
+// keeps the fragment reads below free of bank conflicts: the eight lanes of a
+// K read (rows 0..7, one logical chunk) and the sixteen of a V read (one row,
+// consecutive 8-byte pieces) each cover 128 distinct bytes of banks.
+constexpr int kLdsTileBytes = 4096;
+
+__device__ __forceinline__ void copy_tile_to_lds(unsigned char *dst, const uint16_t *kc,
+                                                 const uint16_t *vc, int64_t block_elems,
+                                                 int tile_off_bytes, int blk, int kvh,
+                                                 int row_bytes, int lane) {
+  const bool ok = blk >= 0;
+  const uint32_t bytes = ok ? static_cast<uint32_t>(block_elems * 2) : 0u;
+  const int64_t base = ok ? (int64_t)blk * block_elems : 0;
+  const __amdgpu_buffer_rsrc_t rk = block_rsrc(kc + base, bytes);
+  const __amdgpu_buffer_rsrc_t rv = block_rsrc(vc + base, bytes);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    const int src_chunk = (lane & 7) ^ (row & 7);
+    const uint32_t off = static_cast<uint32_t>(row * row_bytes + kvh * 128 + 16 * src_chunk);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t *)(dst + 1024 * i), 16, off,
+                                             tile_off_bytes, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t *)(dst + 2048 + 1024 * i), 16, off,
+                                             tile_off_bytes, 0, 0);
+  }
+}
+
+// The register fragments of a tile landed by copy_tile_to_lds, in the layout
+// load_tile gives them (head_dim 64).
+__device__ __forceinline__ void read_tile_from_lds(Tile<64> &t, const unsigned char *src,
+                                                   int blk, int rel, int m16, int g) {
+  t.blk = blk;
+  t.rel = rel;
+  t.sub = -1;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)  // K row m16, elements 32j + 8g .. +8
+    t.k[j] = *reinterpret_cast<const uint4 *>(src + m16 * 128 + 16 * ((4 * j + g) ^ (m16 & 7)));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // V row 4g + i, elements 4 m16 .. +4
+    const int row = 4 * g + i;
+    t.v[i] = *reinterpret_cast<const uint2 *>(src + 2048 + row * 128 +
+                                              16 * ((m16 >> 1) ^ (row & 7)) + 8 * (m16 & 1));
+  }
+}
+
 // With kAppend, row t.sub of the tile (if any) takes the appended token's K
 // and V rows, staged in LDS (new_row: K row then V row), in place of what was
 // read from the cache; the substitution is a per-lane select at compute time,
@@ -274,32 +334,94 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
   }
 }
 
-template <int D, int kBatch, bool kDouble, bool kAppend>
-__global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Where one work item lies: sequence b, split, the sequence's clamped
+// context length and split count, and the number of items of the launch.
+struct WorkItem {
+  int b;      // -1: past the last live item
+  int split;
+  int ctx;
+  int ns;
+  int total;  // live (sequence, split) items over the whole batch
+};
+
+// Work items are the live (sequence, split) pairs, sequence-major: item j is
+// split j - first(b) of the sequence b whose items cover j, where sequence b
+// has ns_b = ceil(ctx_b / ts) items. Every wave derives the same answer from
+// the context lengths (64 per round trip), so no workgroup is spent on a
+// split past its sequence's end, and no host-side prefix is needed.
+__device__ __forceinline__ WorkItem find_item(const DecodeParams &p, int j, int64_t cap) {
+  const int lane = threadIdx.x & 63;
+  WorkItem it{-1, 0, 0, 0, 0};
+  int carry = 0;
+  for (int c0 = 0; c0 < p.batch; c0 += 64) {
+    const int idx = c0 + lane;
+    int64_t c = idx < p.batch ? p.ctx[idx] : 0;
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    const int ctx = static_cast<int>(c);  // < 2^31 on this path
+    const int ns = (ctx + p.ts - 1) / p.ts;
+    const int incl = carry + wave_inclusive_scan(ns);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    if (it.b < 0 && j >= carry && j < total) {  // uniform: the item lies in this chunk
+      // Sequences wholly before item j are the lanes whose prefix is <= j
+      // (the prefix is non-decreasing; lanes past the batch carry the total).
+      const int bl = __popcll(__ballot(incl <= j));
+      it.b = c0 + bl;
+      it.ns = __builtin_amdgcn_readlane(ns, bl);
+      it.split = j - (__builtin_amdgcn_readlane(incl, bl) - it.ns);
+      it.ctx = __builtin_amdgcn_readlane(ctx, bl);
+    }
+    carry = total;
+  }
+  it.total = carry;
+  return it;
+}
+
+// Device-coherent stores and loads of the split partials (the sc1 cache
+// policy, bit 4 of the buffer intrinsics' aux operand on gfx950): stores are
+// written through to memory and loads are not served from a possibly stale
+// L2 line, so a workgroup on any XCD reads what another wrote once the
+// writer's stores completed and the group counter moved. Plain buffer loads,
+// not atomic ones: relaxed atomic loads whose addresses might alias are
+// issued one at a time, these are issued back to back.
+constexpr int kCoherent = 16;
+__device__ __forceinline__ void store_shared(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kCoherent);
+}
+__device__ __forceinline__ float load_shared(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCoherent));
+}
+
+// One work item (a split of one sequence, one KV head) for the workgroup.
+template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds>
+__device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkItem &it,
+                                            int kvh) {
   constexpr int QK = D / 32;
   constexpr int VC = D / 16;
-
-  // Grid (KV head, batch, split): split is the slowest dimension, so the
-  // dispatcher hands out every sequence's first split before any later one
-  // and the workgroups of splits past short contexts (which exit at once)
-  // come last. The KV heads of one (sequence, split) are adjacent and start
-  // together, so the halves of the same slot rows are read at about the same
-  // time (measured: 8 x 32K decode 113 -> 109 us, 4K batch-64 step -0.1 us).
-  const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
   const int lane = threadIdx.x & 63;
   // The wave index is uniform within a wave; saying so keeps every value
   // derived from it (tile counts, block ids, descriptors) in SGPRs.
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m16 = lane & 15, g = lane >> 4;
-
+  const int b = it.b, split = it.split, nsplits = it.ns;
+  const int64_t ctx = it.ctx;
   const int64_t t0 = static_cast<int64_t>(split) * p.ts;
   const int64_t *bt_row = p.bt + b * p.bt_stride;
 
-  // Prologue: the context length, the Q fragments and the first 64 block ids
-  // of this wave do not depend on one another, so all three loads are issued
-  // before any is used (one memory latency). Block ids are read for every
-  // tile position the split could hold, within the table's width.
-  const int64_t ctx_raw = p.ctx[b];
+  // Prologue: the Q fragments and the first 64 block ids of this wave do not
+  // depend on one another, so both loads are issued before either is used.
+  // Block ids are read for every tile position the split could hold, within
+  // the table's width.
   const bool head_ok = m16 < p.group;
   const uint16_t *qrow = static_cast<const uint16_t *>(p.q) + b * p.q_sb +
                          (int64_t)(kvh * p.group + (head_ok ? m16 : 0)) * p.q_sh;
@@ -338,12 +460,8 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
         static_cast<const uint16_t *>(new_is_v ? p.new_v : p.new_k) + b * p.new_sb +
         (int64_t)kvh * p.new_sh + new_off);
 
-  const int64_t cap = p.max_blocks * p.block_size;
-  const int64_t ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
-  if (t0 >= ctx) return;  // uniform over the workgroup
   const int64_t t1 = min<int64_t>(ctx, t0 + p.ts);
   const int ntiles = static_cast<int>(ceil_div(t1 - t0, 16));
-  const int nsplits = static_cast<int>(ceil_div(ctx, p.ts));
 
   // Q^T as the B operand: lane l holds Q[head l%16][32j + 8g .. +8).
   bf16x8_t qf[QK];
@@ -454,6 +572,27 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
       issue(bufA, kb + 2 * kBatch);
       compute(bufB);
     }
+  } else if constexpr (kLds) {
+    // Five tiles per wave (320-token splits): four in registers and the
+    // fifth in this wave's LDS slot, all issued up front, so that one
+    // workgroup keeps 80 KB in flight and the splits of a batch like 64
+    // sequences of up to 4K tokens fit the GPU in one generation.
+    static_assert(D == 64 && kBatch == 4, "LDS landing is laid out for head_dim 64");
+    __shared__ __align__(16) unsigned char lds_tiles[kWaves][kLdsTileBytes];
+    Tile<D> buf[kBatch];
+    issue(buf, 0);
+    const int rel4 = 16 * (w + kWaves * kBatch);
+    const int blk4 = kBatch < nk ? __builtin_amdgcn_readlane(blk_reg, kBatch) : -1;
+    copy_tile_to_lds(lds_tiles[w], kc, vc, block_elems,
+                     static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel4)) * row_elems * 2,
+                     blk4, kvh, row_elems * 2, lane);
+    if (append_here) stage_new_row();
+    compute(buf);
+    if (kBatch < nk) {  // uniform
+      read_tile_from_lds(buf[0], lds_tiles[w], blk4, rel4, m16, g);
+      if (append_here && rel4 == last_rel) mark_new_row(buf[0]);
+      compute_tile<D, kAppend>(st, buf[0], qf, scale, live, g, m16, new_row_s);
+    }
   } else {
     // Issued whatever nk is (absent tiles read zeros), so that every path
     // reaching the computes has the same loads in flight.
@@ -485,11 +624,22 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
   __syncthreads();
 
   // Merge the four waves. A sequence that fits one split is finished here;
-  // otherwise the split's (m, l, acc) go to the workspace for the combine
-  // kernel (m as a base-2 exponent).
+  // otherwise the split's (m, l, acc) go to the workspace (m as a base-2
+  // exponent) and the last split of the (sequence, KV head) to finish merges
+  // them all.
   const int head0 = kvh * p.group;
   uint16_t *out = static_cast<uint16_t *>(p.out);
-  float *ws_acc = static_cast<float *>(p.ws_acc);
+  // This group's partial rows: (m, l) pairs and acc rows for its heads h and
+  // splits s at row h * max_splits + s, under buffer resources of the group's
+  // span (at most 16 heads x 8192 splits x 128 dims of FP32: 32-bit offsets).
+  const int64_t row_b = (int64_t)b * p.hq + head0;
+  const int rows_g = p.group * p.max_splits;
+  const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(
+      static_cast<float *>(p.ws_acc) + row_b * p.max_splits * D, 0,
+      static_cast<uint32_t>(rows_g) * D * 4u, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ml_r = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<float *>(p.ws_ml) + row_b * p.max_splits * 2, 0,
+      static_cast<uint32_t>(rows_g) * 8u, 0x00020000);
   for (int idx = threadIdx.x; idx < p.group * D; idx += blockDim.x) {
     const int h = idx / D, d = idx % D;
     float M = m_s[0][h];
@@ -505,74 +655,148 @@ __global__ __launch_bounds__(256) void decode_split_mfma(DecodeParams p) {
     if (nsplits == 1) {
       out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num / den);
     } else {
-      const int64_t row = ((int64_t)b * p.hq + head0 + h) * p.max_splits + split;
-      ws_acc[row * D + d] = num;
-      if (d == 0) p.ws_ml[row] = make_float2(M, den);
+      const uint32_t row = static_cast<uint32_t>(h * p.max_splits + split);
+      store_shared(acc_r, (row * D + d) * 4u, num);
+      if (d == 0) {
+        store_shared(ml_r, row * 8u, M);
+        store_shared(ml_r, row * 8u + 4u, den);
+      }
+    }
+  }
+  if (nsplits == 1) return;
+
+  // Arrival: every thread's partial stores have completed before the group
+  // counter moves. On gfx9 stores count in vmcnt, so waiting for vmcnt(0)
+  // waits for their acknowledgement at device scope (the stores are
+  // write-through); a workgroup-scope fence would not wait for them. The
+  // workgroup that brings the counter to nsplits - 1 is the last and returns
+  // it to zero for the next call (it is the counter's last user in this one).
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ int last_s;
+  if (threadIdx.x == 0) {
+    int *ctr = p.ws_ctr + b * p.hkv + kvh;
+    const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_s = old == nsplits - 1;
+    if (old == nsplits - 1)
+      __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last_s) return;
+
+  // The group merge, in split order whatever the arrival order (the result
+  // does not depend on which split finished last):
+  //   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s,
+  // kChunk splits per memory round trip, chunks after the first rescaling
+  // the running sums.
+  constexpr int kChunk = 16;
+  __shared__ float f_s[kChunk][16];    // 2^{m_s - M_new} of the chunk's splits
+  __shared__ float rescale_s[16];      // 2^{M_old - M_new} per head
+  __shared__ float den_s[16];
+  __shared__ float mrun_s[16];
+  if (threadIdx.x < 16) {
+    den_s[threadIdx.x] = 0.f;
+    mrun_s[threadIdx.x] = -INFINITY;
+  }
+  constexpr int kMaxOut = (16 * D + 255) / 256;  // outputs per thread, at most
+  // Outputs per thread whose partial rows are in flight together: two cover
+  // every group of up to 512 outputs (group * head_dim) in one pass.
+  constexpr int kPre = 2;
+  const int nout = p.group * D;
+  float num[kMaxOut];
+#pragma unroll
+  for (int r = 0; r < kMaxOut; ++r) num[r] = 0.f;
+  for (int s0 = 0; s0 < nsplits; s0 += kChunk) {
+    const int cnt = min(kChunk, nsplits - s0);
+#pragma unroll
+    for (int pass = 0; pass < kMaxOut / kPre; ++pass) {
+      if (pass * kPre * 256 >= nout) break;  // uniform
+      // Partial rows of this pass's outputs; on the first pass they are
+      // issued before the chunk's weights are known. Every load is issued
+      // (outputs past the group read head 0's row, rows past cnt repeat the
+      // last one: in bounds, and their weight is zero or they are not used),
+      // so that all of them are in flight together.
+      float a[kPre][kChunk];
+#pragma unroll
+      for (int r = 0; r < kPre; ++r) {
+        const int idx = threadIdx.x + 256 * (pass * kPre + r);
+        const int h = idx < nout ? idx / D : 0, d = idx % D;
+#pragma unroll
+        for (int s = 0; s < kChunk; ++s) {
+          const uint32_t row = static_cast<uint32_t>(h * p.max_splits + s0 + min(s, cnt - 1));
+          a[r][s] = load_shared(acc_r, (row * D + d) * 4u);
+        }
+      }
+      if (pass == 0) {
+        // The chunk's (m, l) per head, loaded by every lane of wave 0 (lanes
+        // past the group read the last head's: no divergent branch around
+        // the loads), in the same round trip as the partial rows above.
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        float m[kChunk], l[kChunk];
+        if (w == 0) {
+          const int hl = min(static_cast<int>(threadIdx.x), p.group - 1);
+#pragma unroll
+          for (int s = 0; s < kChunk; ++s) {
+            const uint32_t row = static_cast<uint32_t>(hl * p.max_splits + s0 + min(s, cnt - 1));
+            m[s] = load_shared(ml_r, row * 8u);
+            l[s] = load_shared(ml_r, row * 8u + 4u);
+          }
+        }
+        __syncthreads();  // the previous chunk's weights are consumed
+        if (threadIdx.x < p.group) {
+          const int h = threadIdx.x;
+          float m_new = mrun_s[h];
+#pragma unroll
+          for (int s = 0; s < kChunk; ++s)
+            if (s < cnt) m_new = fmaxf(m_new, m[s]);
+          const float rs = __builtin_amdgcn_exp2f(mrun_s[h] - m_new);  // 0 on the first chunk
+          float den = den_s[h] * rs;
+#pragma unroll
+          for (int s = 0; s < kChunk; ++s) {
+            const float f = s < cnt ? __builtin_amdgcn_exp2f(m[s] - m_new) : 0.f;
+            f_s[s][h] = f;
+            den += f * l[s];
+          }
+          rescale_s[h] = rs;
+          den_s[h] = den;
+          mrun_s[h] = m_new;
+        }
+        __syncthreads();
+      }
+#pragma unroll
+      for (int r = 0; r < kPre; ++r) {
+        const int idx = threadIdx.x + 256 * (pass * kPre + r);
+        if (idx < nout) {
+          const int h = idx / D;
+          float acc = num[pass * kPre + r] * rescale_s[h];
+#pragma unroll
+          for (int s = 0; s < kChunk; ++s) acc += f_s[s][h] * a[r][s];  // f = 0 past cnt
+          num[pass * kPre + r] = acc;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kMaxOut; ++r) {
+    const int idx = threadIdx.x + 256 * r;
+    if (idx < p.group * D) {
+      const int h = idx / D, d = idx % D;
+      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] =
+          float_to_bf16_bits(num[r] / den_s[h]);
     }
   }
 }
 
-// Pass 2 for the bf16 kernel: one wave per (query head, sequence) merges the
-// splits; sequences with one split are already done. Splits go in chunks of
-// kChunk: the chunk's (m, l) (lane s holds split s) and acc rows (lane d holds
-// dims d, d+64) are all loaded before any arithmetic, so a chunk costs one
-// memory latency; chunks after the first rescale the running sums.
-template <int D>
-__global__ __launch_bounds__(64) void decode_combine_mfma(DecodeParams p) {
-  constexpr int kChunk = 16;
-  constexpr int C = D / 64;
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int lane = threadIdx.x;
-  const float *ws_acc = static_cast<const float *>(p.ws_acc);
-  const int64_t row0 = ((int64_t)b * p.hq + h) * p.max_splits;
-  // Loads of chunk s0: rows past the last split repeat it (in bounds; their
-  // weight is zero). Unconditional, so that they issue back to back.
-  float a[kChunk][C];
-  float2 ml_raw;
-  auto load_chunk = [&](int s0, int last) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      const int64_t row = row0 + min(s0 + j, last);
-#pragma unroll
-      for (int c = 0; c < C; ++c) a[j][c] = ws_acc[row * D + 64 * c + lane];
-    }
-    ml_raw = p.ws_ml[row0 + min(s0 + lane, last)];
-  };
-  // The first chunk goes out with the context length: one round trip for a
-  // sequence of at most kChunk splits.
-  load_chunk(0, p.max_splits - 1);
+// One workgroup per (live item, KV head). The KV heads of one (sequence,
+// split) are adjacent workgroups, so both halves of the same slot rows are
+// read at about the same time; the grid is sized for the widest table and the
+// workgroups past the live items exit after the context lengths.
+template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds>
+__global__ __launch_bounds__(256) void decode_mfma(DecodeParams p) {
   const int64_t cap = p.max_blocks * p.block_size;
-  int64_t ctx = p.ctx[b];
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int ns = static_cast<int>(ceil_div(ctx, p.ts));
-  if (ns <= 1) return;
-  float num[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) num[c] = 0.f;
-  float den = 0.f, M = -INFINITY;
-  for (int s0 = 0; s0 < ns; s0 += kChunk) {
-    if (s0 > 0) load_chunk(s0, ns - 1);
-    const int cnt = min(kChunk, ns - s0);
-    // Lane s < cnt holds split s0 + s; only lanes 0..15 take part.
-    const float2 ml = lane < cnt ? ml_raw : make_float2(-INFINITY, 0.f);
-    const float m_new = fmaxf(M, lane_value(row_max16(ml.x), 0));
-    const float rescale = __builtin_amdgcn_exp2f(M - m_new);  // 0 on the first chunk
-    const float f = __builtin_amdgcn_exp2f(ml.x - m_new);
-    den = den * rescale + lane_value(row_sum16(f * ml.y), 0);
-    M = m_new;
-#pragma unroll
-    for (int c = 0; c < C; ++c) num[c] *= rescale;
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      const float fj = lane_value(f, j);
-      // A select, not a product: rows past cnt may hold anything.
-#pragma unroll
-      for (int c = 0; c < C; ++c) num[c] += j < cnt ? fj * a[j][c] : 0.f;
-    }
-  }
-  uint16_t *out = static_cast<uint16_t *>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
-#pragma unroll
-  for (int c = 0; c < C; ++c) out[64 * c + lane] = float_to_bf16_bits(num[c] / den);
+  const WorkItem it = find_item(p, blockIdx.x / p.hkv, cap);
+  if (it.b < 0) return;  // uniform
+  decode_item<D, kBatch, kDouble, kAppend, kLds>(p, it, blockIdx.x % p.hkv);
 }
 
 }  // namespace
@@ -583,38 +807,40 @@ bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
          group >= 1 && group <= 16 && block_size % 16 == 0;
 }
 
+template <int D, int B, bool DB, bool A, bool L>
+int launch_one(const DecodeParams &p, hipStream_t stream) {
+  // Every (sequence, split) item that can exist, times the KV heads.
+  const int64_t items = (int64_t)p.batch * p.max_splits * p.hkv;
+  if (items > 0x7fffffff)
+    return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_decode: %lld work items exceed the grid",
+                     (long long)items);
+  decode_mfma<D, B, DB, A, L><<<dim3(static_cast<unsigned>(items)), 256, 0, stream>>>(p);
+  return check_launch("mlr_paged_decode(mfma)");
+}
+
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
-  dim3 grid(p.hkv, p.batch, p.max_splits);
   // Tiles per wave: ceil(ts / 16 / 4). A split whose tiles fit one load batch
-  // needs no second register buffer (fewer VGPRs, more waves per SIMD).
+  // needs no second register buffer (fewer VGPRs, more waves per SIMD); at
+  // head_dim 64 a 320-token split lands its fifth tile per wave in LDS.
   const int tiles_per_wave = static_cast<int>(ceil_div(ceil_div(p.ts, 16), kWaves));
   const bool append = p.new_k != nullptr;
-  // Instantiations: head_dim x (one load batch | double-buffered) x append.
-#define MLR_SPLIT(D_, B_, DB_)                                            \
-  (append ? (decode_split_mfma<D_, B_, DB_, true><<<grid, 256, 0, stream>>>(p)) \
-          : (decode_split_mfma<D_, B_, DB_, false><<<grid, 256, 0, stream>>>(p)))
+  // Instantiations: head_dim x (one load batch | + LDS tile | double-buffered) x append.
   if (p.d == 64) {
     if (tiles_per_wave <= 4)
-      MLR_SPLIT(64, 4, false);
-    else
-      MLR_SPLIT(64, 4, true);
-  } else {
-    if (tiles_per_wave <= 2)
-      MLR_SPLIT(128, 2, false);
-    else
-      MLR_SPLIT(128, 2, true);
+      return append ? launch_one<64, 4, false, true, false>(p, stream)
+                    : launch_one<64, 4, false, false, false>(p, stream);
+    if (p.ts == kLdsSplit64)
+      return append ? launch_one<64, 4, false, true, true>(p, stream)
+                    : launch_one<64, 4, false, false, true>(p, stream);
+    return append ? launch_one<64, 4, true, true, false>(p, stream)
+                  : launch_one<64, 4, true, false, false>(p, stream);
   }
-#undef MLR_SPLIT
-  int rc = check_launch("mlr_paged_decode(split, mfma)");
-  if (rc != MLR_OK) return rc;
-  if (p.max_splits <= 1) return MLR_OK;  // every sequence fits one split
-  dim3 cgrid(p.hq, p.batch);
-  if (p.d == 64) {
-    decode_combine_mfma<64><<<cgrid, 64, 0, stream>>>(p);
-  } else {
-    decode_combine_mfma<128><<<cgrid, 64, 0, stream>>>(p);
-  }
-  return check_launch("mlr_paged_decode(combine, mfma)");
+  if (tiles_per_wave <= 2)
+    return append ? launch_one<128, 2, false, true, false>(p, stream)
+                  : launch_one<128, 2, false, false, false>(p, stream);
+  return append ? launch_one<128, 2, true, true, false>(p, stream)
+                : launch_one<128, 2, true, false, false>(p, stream);
 }
 
 }  // namespace mlr
+

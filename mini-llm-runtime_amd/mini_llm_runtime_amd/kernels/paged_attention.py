@@ -53,6 +53,26 @@ def _require_kernel_layout(q: torch.Tensor, k_cache: torch.Tensor,
         raise TypeError(f"{what}: q, k_cache and v_cache must share one dtype")
 
 
+# Decode workspaces by (device, stream): zero-filled when allocated. The
+# matrix-core decode keeps per-(sequence, KV head) arrival counters at the
+# front of the workspace; they must be zero when a call starts, and every call
+# leaves them zero. One workspace per stream keeps calls on different streams
+# from sharing counters or partials.
+_WORKSPACES: dict = {}
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A zero-initialised decode workspace of at least `nbytes` for the
+    current stream of `device`, reused across calls."""
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int,
                            max_context: int, dtype: torch.dtype,
                            tokens_per_split: int = 0) -> int:
@@ -77,6 +97,9 @@ def paged_decode_launch(q: torch.Tensor, k_cache: torch.Tensor,
     With new_k/new_v [B, Hkv, D] (cache dtype) and slot_mapping [B] int64, the
     decode step's KV write happens in the same call (mlr_paged_decode_append):
     slot_mapping[b] must be the slot of position seq_lens[b] - 1.
+    A caller-provided `workspace` (uint8, at least decode_workspace_bytes)
+    must be all-zero before its first use; each call leaves it reusable.
+    Calls that share a workspace must not overlap.
     """
     device = _lib.require_hip(q, k_cache, v_cache, block_tables, seq_lens,
                               what="paged decode")
@@ -100,8 +123,11 @@ def paged_decode_launch(q: torch.Tensor, k_cache: torch.Tensor,
     dcode = _lib.dtype_code(q.dtype, "paged decode")
     ws_bytes = int(lib.mlr_paged_decode_workspace_size(
         batch, num_q_heads, head_dim, width * block_size, tokens_per_split, dcode))
-    if workspace is None or workspace.numel() < ws_bytes:
-        workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
+    if workspace is None:
+        workspace = decode_workspace(device, ws_bytes)
+    elif workspace.numel() < ws_bytes:
+        raise ValueError(f"decode workspace of {workspace.numel()} bytes is smaller than "
+                         f"the {ws_bytes} bytes required")
     stream = _lib.stream_handle(device)
     common = (q.data_ptr(), q.stride(0), q.stride(1),
               k_cache.data_ptr(), v_cache.data_ptr(),

@@ -277,3 +277,58 @@ def test_per_request_loop_qwen05b_shape(device, dtype):
         q.to(device), kc.to(device), vc.to(device), tables, lens, 16)
     assert torch.isfinite(got).all()
     assert max_abs(got, want) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("tokens_per_split", [0, 64, 272])
+def test_single_launch_merge_reuses_its_workspace(device, tokens_per_split):
+    """The matrix-core decode merges a sequence's splits in the same launch
+    (the last split to finish merges them, through per-(sequence, KV head)
+    counters in the workspace). Five calls with fresh inputs on one workspace:
+    each matches the oracle, and every counter is back at zero after each."""
+    lens = [1, 16, 17, 255, 256, 257, 1000, 2049, 4096, 3000, 40, 700]
+    batch, hq, hkv = len(lens), 14, 2
+    ws_bytes = kpa.decode_workspace_bytes(batch, hq, 64, 4096, torch.bfloat16,
+                                          tokens_per_split)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)
+    for seed in range(5):
+        q, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, 64, 16, dtype=torch.bfloat16,
+                                                 seed=100 + seed)
+        width = bt.shape[1]
+        bt = torch.nn.functional.pad(bt, (0, 256 - width), value=-1)  # 4096-token tables
+        want = opa.decode_batch_loop(q, kc, vc, tables, lens, 16)
+        got = kpa.paged_decode_launch(q.to(device), kc.to(device), vc.to(device),
+                                      bt.to(device), sl.to(device),
+                                      tokens_per_split=tokens_per_split, workspace=ws)
+        assert torch.isfinite(got).all()
+        assert max_abs(got, want) <= 2e-2, seed
+        counters = ws[:batch * hq * 4].view(torch.int32)
+        assert int(counters.abs().sum()) == 0, seed
+
+
+def test_single_launch_merge_in_graph_replays(device):
+    """A captured decode replayed several times, with new queries copied in
+    eagerly between replays: every replay equals an eager call bit for bit
+    (the counters the merge uses return to zero inside each replay)."""
+    lens = [33, 600, 1500, 4000, 257]
+    q, kc, vc, bt, sl, _ = random_paged(lens, 14, 2, 64, 16, dtype=torch.bfloat16, seed=77)
+    q, kc, vc, bt, sl = (t.to(device) for t in (q, kc, vc, bt, sl))
+    out = torch.empty_like(q)
+    ws = torch.zeros(kpa.decode_workspace_bytes(5, 14, 64, bt.shape[1] * 16, torch.bfloat16),
+                     dtype=torch.uint8, device=device)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        kpa.paged_decode_launch(q, kc, vc, bt, sl, out, workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        kpa.paged_decode_launch(q, kc, vc, bt, sl, out, workspace=ws)
+    gen = torch.Generator().manual_seed(3)
+    for _ in range(4):
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(device))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = kpa.paged_decode_launch(q, kc, vc, bt, sl)
+        assert torch.equal(replayed, eager)
