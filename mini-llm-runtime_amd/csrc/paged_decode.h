@@ -40,8 +40,12 @@ struct DecodeParams {
   void *vc_w;
 };
 
-// Workspace: arrival counters (zero between calls), then the split partials
-// (m, l) and acc, each part 256-byte aligned.
+// Workspace: a fixed region of arrival counters (zero between calls), then
+// the split partials (m, l) and acc, each 256-byte aligned. The counter
+// region has the same size for every call, so the partials of one call never
+// land where a later call with another shape keeps its counters.
+constexpr int64_t kCounterSlots = 65536;  // (sequence, KV head) pairs, at most
+constexpr int64_t kCounterBytes = kCounterSlots * 4;
 struct DecodeWorkspace {
   int64_t ml_offset;
   int64_t acc_offset;

@@ -233,9 +233,7 @@ int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_contex
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype) {
   DecodeWorkspace w;
-  // One arrival counter per (sequence, KV head); hq bounds the KV head count.
-  const int64_t ctr_bytes = batch * hq * static_cast<int64_t>(sizeof(int));
-  w.ml_offset = (ctr_bytes + 255) / 256 * 256;
+  w.ml_offset = kCounterBytes;
   const int64_t rows = batch * hq * max_splits;
   const int64_t ml_bytes = rows * static_cast<int64_t>(sizeof(float2));
   w.acc_offset = w.ml_offset + (ml_bytes + 255) / 256 * 256;
@@ -310,8 +308,10 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                        (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 &&
                        q_stride_b % 8 == 0 && q_stride_h % 8 == 0;
   // The matrix-core kernel keeps token positions in 32 bits.
+  // The matrix-core kernel keeps one arrival counter per (sequence, KV head)
+  // in the workspace's fixed counter region.
   const bool mfma =
-      aligned && max_context < (int64_t(1) << 31) &&
+      aligned && max_context < (int64_t(1) << 31) && batch * num_kv_heads <= kCounterSlots &&
       decode_mfma_eligible(dtype, head_dim, num_q_heads / num_kv_heads, block_size);
   int64_t ts = tokens_per_split > 0 ? tokens_per_split
                                     : default_tokens_per_split(mfma, head_dim, max_context);
@@ -443,3 +443,4 @@ extern "C" int mlr_paged_decode_append(
                     workspace_bytes, out, out_stride_b, out_stride_h, stream,
                     &app);
 }
+

@@ -301,7 +301,7 @@ def test_single_launch_merge_reuses_its_workspace(device, tokens_per_split):
                                       tokens_per_split=tokens_per_split, workspace=ws)
         assert torch.isfinite(got).all()
         assert max_abs(got, want) <= 2e-2, seed
-        counters = ws[:batch * hq * 4].view(torch.int32)
+        counters = ws[:65536 * 4].view(torch.int32)
         assert int(counters.abs().sum()) == 0, seed
 
 
@@ -332,3 +332,27 @@ def test_single_launch_merge_in_graph_replays(device):
         replayed = out.clone()
         eager = kpa.paged_decode_launch(q, kc, vc, bt, sl)
         assert torch.equal(replayed, eager)
+
+
+def test_workspace_survives_calls_of_other_shapes(device):
+    """One workspace through calls of different batch sizes, head layouts,
+    dtypes (the generic kernel writes partials too) and split sizes, large
+    then small then large again: every call matches the oracle and the
+    counter region is zero after each (partials never land on counters)."""
+    ws = torch.zeros(kpa.decode_workspace_bytes(64, 28, 128, 8192, torch.bfloat16, 16),
+                     dtype=torch.uint8, device=device)
+    calls = [
+        ([4096, 300, 2000, 17] * 8, 14, 2, 64, torch.bfloat16, 0),
+        ([40, 900], 14, 2, 64, torch.float32, 16),
+        ([33, 257], 8, 8, 64, torch.bfloat16, 16),
+        ([700, 1500, 64], 28, 4, 128, torch.bfloat16, 0),
+        ([4096, 300, 2000, 17] * 8, 14, 2, 64, torch.bfloat16, 0),
+        ([3000, 1] * 16, 14, 2, 64, torch.bfloat16, 64),
+    ]
+    for i, (lens, hq, hkv, d, dtype, ts) in enumerate(calls):
+        q, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, 16, dtype=dtype, seed=40 + i)
+        want = opa.decode_batch_loop(q, kc, vc, tables, lens, 16)
+        got = kpa.paged_decode_launch(q.to(device), kc.to(device), vc.to(device), bt.to(device),
+                                      sl.to(device), tokens_per_split=ts, workspace=ws)
+        assert max_abs(got, want) <= TOL[dtype], i
+        assert int(ws[:65536 * 4].view(torch.int32).abs().sum()) == 0, i
