@@ -161,6 +161,31 @@ int mlr_paged_decode_append(
     int64_t out_stride_h, void *stream);
 
 /*
+ * mlr_paged_decode_append without a workspace argument: the decode scratch
+ * (split counters and partials) is an 8 MiB array the library keeps on each
+ * GPU it runs on, so the call allocates nothing. It has no counterpart in the
+ * reference; it is for callers that cannot allocate device memory, such as
+ * code under graph capture or a serving loop that forbids allocation.
+ *   - Sizes whose scratch would pass 8 MiB are rejected (MLR_ERR_WORKSPACE)
+ *     before anything is launched or written; mlr_paged_decode_workspace_size
+ *     gives the need (e.g. 64 sequences x 28 query heads x 16 splits of
+ *     head_dim 128 fit).
+ *   - Every call on one GPU shares that GPU's array: calls that overlap on one
+ *     GPU (other streams, other threads) race and must not be issued.
+ *   - Arguments, results and cache contents are those of
+ *     mlr_paged_decode_append with the same inputs (the same kernels run).
+ */
+int mlr_paged_decode_append_static(
+    const void *q, int64_t q_stride_b, int64_t q_stride_h, void *k_cache,
+    void *v_cache, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+    int64_t head_dim, const int64_t *block_tables, int64_t block_table_stride,
+    int64_t max_blocks_per_seq, const int64_t *context_lens, int64_t batch,
+    int64_t num_q_heads, double scale, int dtype, int64_t tokens_per_split,
+    const void *new_k, const void *new_v, int64_t new_stride_b,
+    int64_t new_stride_h, const int64_t *slot_mapping, void *out,
+    int64_t out_stride_b, int64_t out_stride_h, void *stream);
+
+/*
  * Paged chunk-prefill attention for a packed batch of sequences (varlen):
  * sequence s owns query rows [query_start_loc[s], query_start_loc[s+1]) of q,
  * whose absolute positions are prefix_len_s + i with

@@ -17,6 +17,8 @@
 // bf16 inputs with head_dim 64 or 128 and at most 16 query heads per KV head
 // take the MFMA kernel in paged_decode_mfma.hip; everything else takes the
 // generic kernel below.
+#include <atomic>
+
 #include "mlr_common.h"
 #include "paged_decode.h"
 
@@ -444,3 +446,77 @@ extern "C" int mlr_paged_decode_append(
                     &app);
 }
 
+// ---------------------------------------------------------------------------
+// mlr_paged_decode_append_static: the decode step with the library's own
+// scratch instead of a caller workspace, for callers that cannot allocate.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Decode scratch of the library on every GPU it runs on: the counter region
+// and the split partials of one call (8 MiB covers, for instance, 64
+// sequences x 28 query heads x 16 splits at head_dim 128). Each device holds
+// its own copy until the process ends. Static device memory starts zeroed, as
+// the counter region must; every call leaves the counters zero again.
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxScratchDevices];
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current. In host code the array's name is only a
+// stand-in for the symbol; kernels must be given this address.
+int scratch_address(void **out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return set_error(MLR_ERR_HIP, "mlr_paged_decode_append_static: hipGetDevice failed: %s",
+                     hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(MLR_ERR_UNSUPPORTED,
+                     "mlr_paged_decode_append_static: device %d is past the %d devices "
+                     "the library keeps scratch addresses for", dev, kMaxScratchDevices);
+  void *ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return set_error(MLR_ERR_HIP,
+                       "mlr_paged_decode_append_static: hipGetSymbolAddress(scratch) "
+                       "failed on device %d: %s", dev, hipGetErrorString(err));
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);  // same value from any thread
+  }
+  *out = ptr;
+  return MLR_OK;
+}
+
+}  // namespace
+
+extern "C" int mlr_paged_decode_append_static(
+    const void *q, int64_t q_stride_b, int64_t q_stride_h, void *k_cache,
+    void *v_cache, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+    int64_t head_dim, const int64_t *block_tables, int64_t block_table_stride,
+    int64_t max_blocks_per_seq, const int64_t *context_lens, int64_t batch,
+    int64_t num_q_heads, double scale, int dtype, int64_t tokens_per_split,
+    const void *new_k, const void *new_v, int64_t new_stride_b, int64_t new_stride_h,
+    const int64_t *slot_mapping, void *out, int64_t out_stride_b,
+    int64_t out_stride_h, void *stream) {
+  clear_error();
+  void *ws = nullptr;
+  int rc = scratch_address(&ws);
+  if (rc != MLR_OK) return rc;
+  const AppendArgs app{new_k, new_v, new_stride_b, new_stride_h, slot_mapping};
+  rc = run_decode(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks, block_size,
+                  num_kv_heads, head_dim, block_tables, block_table_stride,
+                  max_blocks_per_seq, context_lens, batch, num_q_heads, scale, dtype,
+                  tokens_per_split, ws, kStaticScratchBytes, out, out_stride_b,
+                  out_stride_h, stream, &app);
+  if (rc == MLR_ERR_WORKSPACE) {
+    char why[384];
+    snprintf(why, sizeof(why), "%s", mlr_last_error());
+    return set_error(MLR_ERR_WORKSPACE,
+                     "mlr_paged_decode_append_static: these sizes need more decode scratch "
+                     "than the library's %zu-byte array (%s); call mlr_paged_decode_append "
+                     "with a workspace instead", kStaticScratchBytes, why);
+  }
+  return rc;
+}

@@ -1,0 +1,105 @@
+"""mlr_paged_decode_append_static (the decode step on the library's own
+scratch, for callers that cannot allocate) against mlr_paged_decode_append
+with a caller workspace, through the C ABI.
+
+The two entry points run the same kernels, so outputs and the K/V written to
+the cache must be identical bit for bit. Two calls in a row, the second with a
+smaller batch (the scratch keeps the first call's contents), then an oversized
+request that must be rejected before anything is launched or written.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from mini_llm_runtime_amd import _lib, workloads
+from mini_llm_runtime_amd.kernels import paged_attention as kpa
+from oracle_pins import random_paged
+
+pytestmark = pytest.mark.gpu
+
+
+def _static_call(q, kc, vc, bt, ctx, new_k, new_v, slots, out, tokens_per_split=0):
+    lib = _lib.load()
+    nb, bs, hkv, d = kc.shape
+    batch, hq, _ = q.shape
+    with torch.cuda.device(q.device):
+        return lib.mlr_paged_decode_append_static(
+            q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), nb, bs, hkv, d,
+            bt.data_ptr(), bt.stride(0), bt.shape[1], ctx.data_ptr(), batch, hq,
+            1.0 / math.sqrt(d), _lib.dtype_code(q.dtype, "decode"), tokens_per_split,
+            new_k.data_ptr(), new_v.data_ptr(), new_k.stride(0), new_k.stride(1),
+            slots.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.stream_handle(q.device))
+
+
+def _check_pair(device, q, kc, vc, bt, ctx, new_k, new_v, slots, tokens_per_split=0):
+    """Static scratch vs caller workspace on copies of the same cache."""
+    k1, v1 = kc.clone(), vc.clone()
+    k2, v2 = kc.clone(), vc.clone()
+    out_static = torch.empty_like(q)
+    rc = _static_call(q, k1, v1, bt, ctx, new_k, new_v, slots, out_static, tokens_per_split)
+    assert rc == 0, _lib.load().mlr_last_error()
+    ws = torch.zeros(kpa.decode_workspace_bytes(q.shape[0], q.shape[1], q.shape[2],
+                                                bt.shape[1] * kc.shape[1], q.dtype,
+                                                tokens_per_split),
+                     dtype=torch.uint8, device=device)
+    out_ws = kpa.paged_decode_launch(q, k2, v2, bt, ctx, workspace=ws, new_k=new_k,
+                                     new_v=new_v, slot_mapping=slots,
+                                     tokens_per_split=tokens_per_split)
+    torch.cuda.synchronize()
+    assert torch.equal(out_static, out_ws)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    return out_static
+
+
+def test_static_scratch_decode_equals_workspace_decode(device):
+    # Call 1: the Qwen2.5-0.5B decode step (64 sequences, contexts U[128, 4096]).
+    wl = workloads.bf16_decode_qwen05b_b64()
+    q, kc, vc, bt, ctx = (t.to(device) for t in (wl.q, wl.k_cache, wl.v_cache,
+                                                  wl.block_tables, wl.context_lens))
+    slots, nk, nv = (t.to(device) for t in (wl.slot_mapping, wl.new_k, wl.new_v))
+    first = _check_pair(device, q, kc, vc, bt, ctx, nk, nv, slots)
+    assert torch.isfinite(first).all()
+    del q, kc, vc, bt, ctx, slots, nk, nv
+
+    # Call 2, smaller: 5 sequences at head_dim 128 (GQA 7), on the same
+    # scratch, which still holds call 1's partials.
+    lens = [1, 17, 300, 1000, 2049]
+    q, kc, vc, bt, sl, tables = random_paged(lens, 28, 4, 128, 16, dtype=torch.bfloat16,
+                                             seed=8, fill=0.0)
+    gen = torch.Generator().manual_seed(9)
+    new_k = torch.randn(len(lens), 4, 128, generator=gen).bfloat16()
+    new_v = torch.randn(len(lens), 4, 128, generator=gen).bfloat16()
+    slots = torch.tensor([tables[b][(n - 1) // 16] * 16 + (n - 1) % 16
+                          for b, n in enumerate(lens)])
+    args = [t.to(device) for t in (q, kc, vc, bt, sl, new_k, new_v, slots)]
+    _check_pair(device, *args)
+    _check_pair(device, *args, tokens_per_split=64)
+
+
+def test_static_scratch_rejects_oversized_requests_before_writing(device):
+    """16 sequences x 16 heads x 4096 splits of head_dim 128 need far more
+    than 8 MiB of scratch: the call fails with MLR_ERR_WORKSPACE, names the
+    limit, and leaves the cache and the output untouched."""
+    lens = [17] * 16
+    q, kc, vc, bt, sl, tables = random_paged(lens, 16, 4, 128, 16, dtype=torch.bfloat16,
+                                             seed=3, fill=0.0)
+    bt = torch.nn.functional.pad(bt, (0, 4095), value=-1)  # 65536-token tables
+    new_k = torch.zeros(16, 4, 128, dtype=torch.bfloat16)
+    new_v = torch.zeros(16, 4, 128, dtype=torch.bfloat16)
+    slots = torch.tensor([tables[b][1] * 16 for b in range(16)])  # position 16
+    q, kc, vc, bt, sl, new_k, new_v, slots = (t.to(device) for t in
+                                              (q, kc, vc, bt, sl, new_k, new_v, slots))
+    before_k = kc.clone()
+    out = torch.full_like(q, 7.0)
+    rc = _static_call(q, kc, vc, bt, sl, new_k, new_v, slots, out, tokens_per_split=16)
+    torch.cuda.synchronize()
+    assert rc == 3  # MLR_ERR_WORKSPACE
+    msg = _lib.load().mlr_last_error().decode()
+    assert "mlr_paged_decode_append_static" in msg and "8388608" in msg
+    assert torch.equal(kc, before_k)
+    assert torch.all(out == 7.0)
