@@ -3,38 +3,44 @@
 One step = the decode step of one attention layer at Qwen2.5-0.5B shape
 (bf16_decode_qwen05b_b64: batch 64, 14 q / 2 KV heads, head_dim 64, block 16,
 contexts U[128, 4096], 24576-block pool): the batched KV write of the 64 new
-tokens through slot_mapping, then split-KV paged decode (split + combine).
+tokens through slot_mapping and the split-KV paged decode, one launch
+(mlr_paged_decode_append: the write folded in, the splits merged in place).
 
 Timing: inputs are resident in HBM. Consecutive steps use consecutive layers
 of a 24-layer cache (24 distinct 201 MB K+V pools, 4.8 GB), so a layer's pool
 is evicted from the 256 MB Infinity Cache (MALL) before it is read again and
-the figure is an HBM figure. The steps are captured once into a HIP graph of
-24 steps and replayed; HIP events on the launch stream bracket exactly
-``--steps`` steps. ``value`` is whole-step algorithmic bytes / time.
+the figure is an HBM figure. Exactly ``--steps`` steps are captured into one
+HIP graph; after at least ``--warmup`` steps and 0.25 s of untimed replays of
+it, one replay is bracketed by HIP events on its stream (with device
+synchronisation on both sides). ``value`` is whole-step algorithmic bytes /
+time; ``config.us_per_step_10_replays`` repeats the graph ten times as a
+cross-check.
 
-The roofline object is for the dominant kernel call, mlr_paged_decode (split
-+ combine kernels): its algorithmic bytes (K and V rows of every context
-token, q, out, block ids, lengths) over its own event-timed average duration,
-against the 8 TB/s HBM peak.
+The roofline object is for that launch: its algorithmic bytes (K and V rows
+of every context token, q, out, block ids, lengths, the written rows) over
+its event-timed average duration, against the 8 TB/s HBM peak.
 
-The CPU baseline times the oracle (a CPU restatement of the reference's
-PyTorch path: write_slots + paged_attention_decode_batch_parallel) on the
-same inputs with all host cores.
+The CPU baselines time the oracle (a CPU restatement of the reference's
+PyTorch path: write_slots + paged_attention_decode_batch_parallel, and
+paged_attention_prefill_chunk_tiled) on the same inputs with all host cores:
+the decode step above, fp32_decode_b4 (FP32, batch 4), and the chunk prefill.
 
-A secondary object reports BF16 chunk prefill (8 x 512-token chunks on
-prefixes U[0, 3584]) in TFLOP/s against the 2.5 PFLOP/s bf16 MFMA peak.
-
-A third, ``serving``, times end-to-end continuous-batching steps of a
-random-init Qwen2.5-0.5B-shape model in BF16 (workloads.qwen05b_serving:
-about 48 decodes + 2 x 1024-token prefills per step, 128 steps after the
-warm-up): ms per step and tokens per second.
+Secondary objects: BF16 chunk prefill (8 x 512-token chunks on prefixes
+U[0, 3584]) in TFLOP/s against the 2.5 PFLOP/s bf16 MFMA peak; the decode
+pair the serving runtime runs (fused pre-attention kernel, then decode); the
+8 x 32K decode over rotated pools; the fused pre-attention step; and
+``serving``, end-to-end continuous-batching steps of a random-init
+Qwen2.5-0.5B-shape model in BF16 (workloads.qwen05b_serving: about 48
+decodes + 2 x 1024-token prefills per step, 128 steps after the warm-up).
+``provenance`` names the sources and library the numbers come from.
 
     python bench.py [--gpus 1] [--steps 240] [--warmup 48]
 
 ``--profile`` launches the same kernels eagerly and untimed, for rocprofv3:
-``--steps`` decode steps over the rotated layers, the prefill call at each KV
-tile, and a plain 1 GiB device copy whose FETCH_SIZE / WRITE_SIZE counters
-calibrate the traffic counters (the copy reads and writes exactly 1 GiB).
+``--steps`` decode steps over the rotated layers, ten prefill calls, the
+fused pre-attention kernel, and a plain 1 GiB device copy whose FETCH_SIZE /
+WRITE_SIZE counters calibrate the traffic counters (the copy reads and
+writes exactly 1 GiB).
 """
 
 from __future__ import annotations
@@ -196,12 +202,10 @@ def profile_run(args, device):
         pbt, qsl, pctx = (t.to(device) for t in (pw.block_tables, pw.query_start_loc,
                                                   pw.context_lens))
         pout = torch.empty_like(pq)
-        for tile in (16, 64, 128):
-            for _ in range(5):
-                kpa.paged_prefill_launch(pq, kc, vc, pbt, qsl, pctx, 512, tile_size=tile,
-                                         out=pout)
+        for _ in range(10):
+            kpa.paged_prefill_launch(pq, kc, vc, pbt, qsl, pctx, 512, tile_size=64, out=pout)
         torch.cuda.synchronize()
-        print("profile: 15 prefill calls", flush=True)
+        print("profile: 10 prefill calls", flush=True)
     if not args.no_pre_attention:
         from mini_llm_runtime_amd.kernels import pre_attention as kpre
         from mini_llm_runtime_amd.model.qwen2_attention import Qwen2RotaryEmbedding
@@ -224,6 +228,21 @@ def profile_run(args, device):
         torch.cuda.synchronize()
         print("profile: 20 fused pre-attention calls (2048 tokens), 10 each at "
               "1/48/512/8192/32768 tokens", flush=True)
+    # 8 x 32K decode over rotated pools (its own kernel instantiation).
+    lw = workloads.bf16_decode_qwen7b_32k()
+    pools = [(lw.k_cache.to(device), lw.v_cache.to(device)) for _ in range(POOLS_32K)]
+    lq, lbt, lctx = lw.q.to(device), lw.block_tables.to(device), lw.context_lens.to(device)
+    lslots, lnk, lnv = (t.to(device) for t in (lw.slot_mapping, lw.new_k, lw.new_v))
+    lout = torch.empty_like(lq)
+    lws = torch.zeros(kpa.decode_workspace_bytes(8, 28, 128, lbt.shape[1] * 16, torch.bfloat16),
+                      dtype=torch.uint8, device=device)
+    for i in range(12):
+        lkc, lvc = pools[i % POOLS_32K]
+        kpa.paged_decode_launch(lq, lkc, lvc, lbt, lctx, lout, workspace=lws, new_k=lnk,
+                                new_v=lnv, slot_mapping=lslots)
+    torch.cuda.synchronize()
+    print(f"profile: 12 decode calls of {lw.name} over {POOLS_32K} pools", flush=True)
+    del pools
     src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -235,8 +254,10 @@ def profile_run(args, device):
 def bench_decode(args, device):
     import torch
 
-    from mini_llm_runtime_amd import _lib, workloads
+    from mini_llm_runtime_amd import workloads
     from mini_llm_runtime_amd.kernels import paged_attention as kpa
+    from mini_llm_runtime_amd.kernels import pre_attention as kpre
+    from mini_llm_runtime_amd.model.qwen2_attention import Qwen2RotaryEmbedding
     from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
 
     wl = workloads.bf16_decode_qwen05b_b64()
@@ -256,17 +277,28 @@ def bench_decode(args, device):
     ts = args.tokens_per_split
     ws_bytes = kpa.decode_workspace_bytes(64, 14, 64, bt.shape[1] * 16, torch.bfloat16, ts)
     workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)
+    # The step the serving runtime runs (Qwen2Attention.forward_decode_batch_with_cache):
+    # the fused pre-attention kernel (bias-free projection output -> rotated q,
+    # rotated k and v written to the cache), then the decode without the
+    # append. Synthetic projection output of the 64 tokens.
+    gen = torch.Generator().manual_seed(64)
+    qkv = torch.randn(64, 18 * 64, generator=gen).to(torch.bfloat16).to(device)
+    positions = (ctx - 1).contiguous()
+    inv_freq = Qwen2RotaryEmbedding(64, 1_000_000.0).inv_freq.to(device)
+    q_rot = torch.empty_like(q)
 
-    def step(layer, with_write=True):
-        # The decode step's KV write is folded into the decode call
-        # (mlr_paged_decode_append); without it, the call is decode only.
+    def step(layer, kind="step"):
         k_layer, v_layer = cache.get_layer_cache(layer)
-        if with_write:
+        if kind == "step":      # KV write folded into the decode (mlr_paged_decode_append)
             kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, tokens_per_split=ts,
                                     workspace=workspace, new_k=new_k, new_v=new_v,
                                     slot_mapping=slots)
-        else:
+        elif kind == "decode":  # decode only
             kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out,
+                                    tokens_per_split=ts, workspace=workspace)
+        else:                   # served pair
+            kpre.qkv_rope_write(qkv, positions, inv_freq, cache, layer, slots, 14, out=q_rot)
+            kpa.paged_decode_launch(q_rot, k_layer, v_layer, bt, ctx, out,
                                     tokens_per_split=ts, workspace=workspace)
 
     stream = torch.cuda.Stream(device)
@@ -274,40 +306,45 @@ def bench_decode(args, device):
     with torch.cuda.stream(stream):
         for layer in range(LAYERS):   # eager warm-up: loads code objects
             step(layer)
+            step(layer, "served")
     torch.cuda.current_stream(device).wait_stream(stream)
     torch.cuda.synchronize()
 
-    graphs = {}
-    for name, with_write in (("step", True), ("decode", False)):
+    def capture(kind, n):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            for layer in range(LAYERS):
-                step(layer, with_write)
-        graphs[name] = g
-    torch.cuda.synchronize()
+            for i in range(n):
+                step(i % LAYERS, kind)
+        return g
 
-    replays = max(1, -(-args.steps // LAYERS))
-    warm = max(1, -(-args.warmup // LAYERS))
-    # At least the requested warm-up, and at least 0.25 s of it, before each
-    # timed region (the clock ramps under sustained load).
-    warm = warm_graph(graphs["step"], stream, warm)
-    t_step = timed_graph(graphs["step"], replays, stream)
-    warm_graph(graphs["decode"], stream, warm)
-    t_decode = timed_graph(graphs["decode"], replays, stream)
-    steps = replays * LAYERS
-    sclk = sample_sclk(graphs["step"].replay)
+    # The headline: exactly --steps steps (consecutive layers, so the MALL
+    # never serves a layer twice) in one graph, after at least --warmup steps
+    # and at least 0.25 s of untimed replays of it; one bracketed replay.
+    steps = max(1, args.steps)
+    g_steps = capture("step", steps)
+    warm = warm_graph(g_steps, stream, max(1, -(-args.warmup // steps)))
+    t_step = timed_graph(g_steps, 1, stream)
+    # A larger sample of the same graph (10 replays) as a cross-check.
+    t_step10 = timed_graph(g_steps, 10, stream) / 10
+    graphs = {kind: capture(kind, LAYERS) for kind in ("decode", "served")}
+    res = {}
+    for kind, g in graphs.items():
+        warm_graph(g, stream)
+        res[kind] = timed_graph(g, 10, stream) / (10 * LAYERS)
+    sclk = sample_sclk(g_steps.replay)
     decode_bytes = wl.algorithmic_bytes()
     step_bytes = decode_bytes + wl.write_bytes()
     sec_per_step = t_step / steps
-    sec_per_decode = t_decode / steps
     return {
         "wl": wl,
         "steps": steps,
-        "warmup": warm * LAYERS,
+        "warmup": warm * steps,
         "ms_per_step": sec_per_step * 1e3,
         "value_gbs": step_bytes / sec_per_step / 1e9,
-        "decode_us": sec_per_decode * 1e6,
-        "decode_gbs": decode_bytes / sec_per_decode / 1e9,
+        "us_per_step_10_replays": t_step10 / steps * 1e6,
+        "decode_us": res["decode"] * 1e6,
+        "decode_gbs": decode_bytes / res["decode"] / 1e9,
+        "served_us": res["served"] * 1e6,
         "decode_bytes": decode_bytes,
         "step_bytes": step_bytes,
         "stream": stream,
@@ -315,7 +352,12 @@ def bench_decode(args, device):
     }
 
 
-def bench_prefill(device, reps=4, calls_per_graph=10):
+def bench_prefill(device, reps=5, calls_per_graph=10):
+    """bf16_prefill_chunk512_x8 through mlr_paged_prefill (varlen, one launch
+    per call). The call passes the reference's tile_size (64); it only orders
+    the FP32 accumulation, and the matrix-core kernel steps by its own 64-key
+    tile whatever it is, so there is one timing: the median over `reps`
+    bracketed replays of a graph of `calls_per_graph` calls."""
     import torch
 
     from mini_llm_runtime_amd import workloads
@@ -330,34 +372,32 @@ def bench_prefill(device, reps=4, calls_per_graph=10):
     bt, qsl, ctx = (t.to(device) for t in (wl.block_tables, wl.query_start_loc,
                                             wl.context_lens))
     out = torch.empty_like(q)
-    results = {}
-    for tile in (16, 64, 128):
-        def call():
-            kpa.paged_prefill_launch(q, kc, vc, bt, qsl, ctx, 512, tile_size=tile, out=out)
-        stream = torch.cuda.Stream(device)
-        stream.wait_stream(torch.cuda.current_stream(device))
-        with torch.cuda.stream(stream):
+
+    def call():
+        kpa.paged_prefill_launch(q, kc, vc, bt, qsl, ctx, 512, tile_size=64, out=out)
+
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        call()
+    torch.cuda.synchronize()
+    # Several back-to-back calls per graph (as consecutive layers run), so
+    # the per-call time is the kernel's, not the graph launch's.
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(calls_per_graph):
             call()
-        torch.cuda.synchronize()
-        # Several back-to-back calls per graph (as consecutive layers run), so
-        # the per-call time is the kernel's, not the graph launch's.
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            for _ in range(calls_per_graph):
-                call()
-        warm_graph(g, stream)
-        secs = timed_graph(g, reps, stream) / (reps * calls_per_graph)
-        results[tile] = secs
-        if tile == 64:
-            sclk = sample_sclk(g.replay)
-    best_tile = min(results, key=results.get)
+    warm_graph(g, stream)
+    times = [timed_graph(g, 1, stream) / calls_per_graph for _ in range(reps)]
+    secs = statistics.median(times)
+    sclk = sample_sclk(g.replay)
     flops = wl.causal_flops()
     return {
         "workload": "bf16_prefill_chunk512_x8",
         "flops_per_call": flops,
-        "us_per_call": {str(t): round(s * 1e6, 2) for t, s in results.items()},
-        "best_tile": best_tile,
-        "tflops": flops / results[best_tile] / 1e12,
+        "us_per_call": round(secs * 1e6, 3),
+        "us_per_call_min_max": [round(min(times) * 1e6, 3), round(max(times) * 1e6, 3)],
+        "tflops": flops / secs / 1e12,
         "wl": wl,
         "sclk": sclk,
     }
@@ -438,20 +478,23 @@ def bench_pre_attention(device, reps=4, calls_per_graph=10):
 
 
 SPLITS_32K = (0, 4, 8, 16, 32, 64)
+POOLS_32K = 3
 
 
-def bench_decode_32k(device, reps=4, calls_per_graph=5):
+def bench_decode_32k(device, reps=4, calls_per_graph=6):
     """Long-context split-KV decode, bf16_decode_qwen7b_32k: 8 sequences of
-    32,768 tokens, 28 q / 4 KV heads, head_dim 128 (537 MB of K/V, above the
-    256 MB MALL), with the step's KV write folded in. Swept over 4/8/16/32
-    splits per sequence and the library's default split size."""
+    32,768 tokens, 28 q / 4 KV heads, head_dim 128, with the step's KV write
+    folded in. Consecutive calls rotate over POOLS_32K copies of the 537 MB
+    K/V pool (1.6 GB in all, beyond the 256 MB MALL), so every call reads
+    HBM. Swept over 4/8/16/32/64 splits per sequence and the library's
+    default split size."""
     import torch
 
     from mini_llm_runtime_amd import workloads
     from mini_llm_runtime_amd.kernels import paged_attention as kpa
 
     wl = workloads.bf16_decode_qwen7b_32k()
-    kc, vc = wl.k_cache.to(device), wl.v_cache.to(device)
+    pools = [(wl.k_cache.to(device), wl.v_cache.to(device)) for _ in range(POOLS_32K)]
     q, bt, ctx = wl.q.to(device), wl.block_tables.to(device), wl.context_lens.to(device)
     slots, new_k, new_v = (t.to(device) for t in (wl.slot_mapping, wl.new_k, wl.new_v))
     out = torch.empty_like(q)
@@ -464,27 +507,32 @@ def bench_decode_32k(device, reps=4, calls_per_graph=5):
                                                     torch.bfloat16, ts),
                          dtype=torch.uint8, device=device)
 
-        def step():
+        def step(i):
+            kc, vc = pools[i % POOLS_32K]
             kpa.paged_decode_launch(q, kc, vc, bt, ctx, out, tokens_per_split=ts,
                                     workspace=ws, new_k=new_k, new_v=new_v,
                                     slot_mapping=slots)
 
         stream.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(stream):
-            step()
+            for i in range(POOLS_32K):
+                step(i)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            for _ in range(calls_per_graph):
-                step()
+            for i in range(calls_per_graph):
+                step(i)
         warm_graph(g, stream)
         us = timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
         sweep["default" if splits == 0 else str(splits)] = round(us, 2)
     best = min(sweep, key=sweep.get)
     best_us = sweep[best]
-    return {"workload": wl.name, "step_bytes": nbytes, "us_by_splits": sweep,
-            "best": best, "GBps": round(nbytes / best_us / 1e3, 1),
-            "frac_of_hbm_peak": round(nbytes / best_us / 1e3 / HBM_PEAK_GBS, 4)}
+    return {"workload": wl.name, "step_bytes": nbytes, "pools_rotated": POOLS_32K,
+            "us_by_splits": sweep, "best": best,
+            "GBps_default": round(nbytes / sweep["default"] / 1e3, 1),
+            "frac_of_hbm_peak_default": round(nbytes / sweep["default"] / 1e3 / HBM_PEAK_GBS, 4),
+            "GBps_best": round(nbytes / best_us / 1e3, 1),
+            "frac_of_hbm_peak_best": round(nbytes / best_us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
 def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=10):
@@ -515,14 +563,50 @@ def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=10):
             "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
+def cpu_model() -> str | None:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _median_runs(fn, budget, min_runs=5, max_runs=50):
+    """One warm-up call, then at least min_runs timed calls (more while the
+    budget in seconds lasts); returns (median seconds, runs)."""
+    fn()
+    times, spent = [], 0.0
+    while len(times) < min_runs or (spent < budget and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        spent += dt
+        if spent > 3 * budget and len(times) >= min_runs:
+            break
+    return statistics.median(times), len(times)
+
+
+def _cpu_threads():
+    import torch
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return torch.get_num_threads()
+
+
 def cpu_baseline_decode(wl, budget):
+    """The reference's CPU path for the decode step (write_slots +
+    paged_attention_decode_batch_parallel, restated by the oracle) on the
+    same inputs."""
     import torch
 
     import oracle.paged_attention as opa
     from oracle.paged_kv_cache import OracleKVCache
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
+    threads = _cpu_threads()
     cache = OracleKVCache(1, wl.k_cache.shape[0], 16, 2, 64, dtype=torch.bfloat16)
     cache.k_cache[0].copy_(wl.k_cache)
     cache.v_cache[0].copy_(wl.v_cache)
@@ -533,55 +617,114 @@ def cpu_baseline_decode(wl, budget):
         opa.decode_batch_parallel(wl.q, k_layer, v_layer, wl.block_tables,
                                   wl.context_lens, 16)
 
-    step()  # warm-up
-    times, spent = [], 0.0
-    while len(times) < 5 or (spent < budget and len(times) < 50):
-        t0 = time.perf_counter()
-        step()
-        dt = time.perf_counter() - t0
-        times.append(dt)
-        spent += dt
-        if spent > 3 * budget:
-            break
-    med = statistics.median(times)
+    med, runs = _median_runs(step, budget)
     return {
         "value": (wl.algorithmic_bytes() + wl.write_bytes()) / med / 1e9,
         "unit": "GB/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"full bf16_decode_qwen05b_b64 step (64-token write_slots + "
                    f"decode_batch_parallel, oracle restatement in PyTorch CPU), "
-                   f"median of {len(times)} runs after 1 warm-up, "
-                   f"{med * 1e3:.1f} ms/step"),
+                   f"median of {runs} runs after 1 warm-up, {med * 1e3:.1f} ms/step"),
+    }
+
+
+def bench_fp32_decode_b4(device, budget):
+    """fp32_decode_b4 (FP32, batch 4, contexts {17, 64, 130, 255}, the new
+    tokens written first): the HIP decode step (mlr_paged_decode_append)
+    against the reference's CPU path (write_slots +
+    paged_attention_decode_batch_parallel, restated by the oracle)."""
+    import torch
+
+    import oracle.paged_attention as opa
+    from mini_llm_runtime_amd import workloads
+    from mini_llm_runtime_amd.kernels import paged_attention as kpa
+    from oracle.paged_kv_cache import OracleKVCache
+
+    wl = workloads.fp32_decode_b4()
+    nbytes = wl.algorithmic_bytes() + wl.write_bytes()
+    kc, vc = wl.k_cache.to(device), wl.v_cache.to(device)
+    q, bt, ctx = wl.q.to(device), wl.block_tables.to(device), wl.context_lens.to(device)
+    slots, nk, nv = (t.to(device) for t in (wl.slot_mapping, wl.new_k, wl.new_v))
+    out = torch.empty_like(q)
+    ws = torch.zeros(kpa.decode_workspace_bytes(4, 14, 64, bt.shape[1] * 16, torch.float32),
+                     dtype=torch.uint8, device=device)
+
+    def call():
+        kpa.paged_decode_launch(q, kc, vc, bt, ctx, out, workspace=ws, new_k=nk, new_v=nv,
+                                slot_mapping=slots)
+
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(10):
+            call()
+    warm_graph(g, stream, seconds=0.1)
+    gpu_us = timed_graph(g, 10, stream) / 100 * 1e6
+
+    threads = _cpu_threads()
+    cache = OracleKVCache(1, wl.k_cache.shape[0], 16, 2, 64, dtype=torch.float32)
+    cache.k_cache[0].copy_(wl.k_cache)
+    cache.v_cache[0].copy_(wl.v_cache)
+
+    def cpu_step():
+        cache.write_slots(wl.slot_mapping, wl.new_k, wl.new_v, 0)
+        k_layer, v_layer = cache.get_layer_cache(0)
+        opa.decode_batch_parallel(wl.q, k_layer, v_layer, wl.block_tables, wl.context_lens, 16)
+
+    med, runs = _median_runs(cpu_step, budget, min_runs=20, max_runs=2000)
+    return {
+        "workload": wl.name,
+        "bytes_per_step": nbytes,
+        "gpu_us_per_step": round(gpu_us, 3),
+        "gpu_GBps": round(nbytes / gpu_us / 1e3, 2),
+        "note": "latency-bound: 0.5 MB per step",
+        "cpu_baseline": {
+            "value": nbytes / med / 1e9,
+            "unit": "GB/s",
+            "us_per_step": round(med * 1e6, 1),
+            "cores": threads,
+            "cpu_model": cpu_model(),
+            "kind": "port",
+            "sample": (f"full fp32_decode_b4 step (write_slots + decode_batch_parallel, "
+                       f"oracle restatement in PyTorch CPU), median of {runs} runs after "
+                       f"1 warm-up"),
+        },
     }
 
 
 def cpu_baseline_prefill(wl, budget):
-    import torch
-
+    """The reference's CPU chunk prefill (paged_attention_prefill_chunk_tiled,
+    tile 64, restated by the oracle) over all 8 sequences of the workload,
+    median of at least 5 passes after one warm-up pass."""
     import oracle.paged_attention as opa
 
+    threads = _cpu_threads()
     kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
     kc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_k)
     vc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_v)
-    flops, spent, seqs = 0, 0.0, 0
-    for s in range(len(wl.prefix_lens)):
-        lo, hi = int(wl.query_start_loc[s]), int(wl.query_start_loc[s + 1])
-        p = wl.prefix_lens[s]
-        t0 = time.perf_counter()
-        opa.prefill_chunk_tiled(wl.q[lo:hi], kc, vc, wl.tables[s], p, p + hi - lo, 16, 64)
-        spent += time.perf_counter() - t0
-        flops += 4 * 64 * 14 * ((hi - lo) * p + (hi - lo) * (hi - lo + 1) // 2)
-        seqs += 1
-        if spent > budget:
-            break
+
+    def all_sequences():
+        for s in range(len(wl.prefix_lens)):
+            lo, hi = int(wl.query_start_loc[s]), int(wl.query_start_loc[s + 1])
+            p = wl.prefix_lens[s]
+            opa.prefill_chunk_tiled(wl.q[lo:hi], kc, vc, wl.tables[s], p, p + hi - lo, 16, 64)
+
+    med, runs = _median_runs(all_sequences, budget, min_runs=5, max_runs=20)
     return {
-        "value": flops / spent / 1e12,
+        "value": wl.causal_flops() / med / 1e12,
         "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": f"{seqs} of 8 sequences of bf16_prefill_chunk512_x8 "
-                  f"(prefill_chunk_tiled, tile 64), {spent:.1f} s",
+        "sample": (f"all 8 sequences of bf16_prefill_chunk512_x8 (prefill_chunk_tiled, "
+                   f"tile 64), median of {runs} passes after 1 warm-up pass, "
+                   f"{med:.2f} s per pass"),
     }
 
 
@@ -660,6 +803,51 @@ def measured_traffic():
         return None
 
 
+def provenance():
+    """What produced this line: the git HEAD when a checkout is present, the
+    sha256 of every kernel source, the ABI header, this script and the built
+    library, and the software and hardware versions."""
+    import glob
+    import hashlib
+    import subprocess
+
+    import torch
+
+    def sha(path):
+        h = hashlib.sha256()
+        with open(path, "rb") as f:
+            for chunk in iter(lambda: f.read(1 << 20), b""):
+                h.update(chunk)
+        return h.hexdigest()
+
+    pkg = os.path.join(REPO, "mini-llm-runtime_amd")
+    files = sorted(glob.glob(os.path.join(pkg, "csrc", "*")) +
+                   glob.glob(os.path.join(REPO, "include", "*.h")) +
+                   [os.path.join(REPO, "bench.py"),
+                    os.path.join(pkg, "mini_llm_runtime_amd", "libmlr_attn.so")])
+    hashes = {os.path.relpath(f, REPO): sha(f)[:16] for f in files if os.path.isfile(f)}
+    combined = hashlib.sha256("".join(f"{k}={v};" for k, v in sorted(hashes.items()))
+                              .encode()).hexdigest()[:16]
+    head = None
+    if os.path.isdir(os.path.join(REPO, ".git")):
+        try:
+            head = subprocess.run(["git", "-C", REPO, "rev-parse", "HEAD"], capture_output=True,
+                                  text=True, timeout=10).stdout.strip() or None
+        except (OSError, subprocess.SubprocessError):
+            head = None
+    props = torch.cuda.get_device_properties(0)
+    return {
+        "git_head": head,
+        "sources_sha256_16": combined,
+        "files_sha256_16": hashes,
+        "torch": torch.__version__,
+        "hip": getattr(torch.version, "hip", None),
+        "gpu": props.name,
+        "gpu_arch": getattr(props, "gcnArchName", None),
+        "cpu_model": cpu_model(),
+    }
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -705,16 +893,21 @@ def main():
             "block_size": 16, "context": "U[128,4096]", "num_blocks": 24576,
             "kv_write_tokens": 64, "layers_rotated": LAYERS,
             "step": ("mlr_paged_decode_append: 64-token KV write fused into the "
-                     "split-KV decode, then the split combine; one layer"),
+                     "split-KV decode, splits merged in the same launch; one layer"),
             "step_bytes": dec["step_bytes"],
             "hbm_pct_of_peak": round(100 * dec["value_gbs"] / HBM_PEAK_GBS, 2),
+            "us_per_step_10_replays": round(dec["us_per_step_10_replays"], 3),
             "decode_only_us": round(dec["decode_us"], 3),
+            "served_step_us": round(dec["served_us"], 3),
+            "served_step": ("what Qwen2Attention.forward_decode_batch_with_cache runs after "
+                            "its QKV GEMM: mlr_qkv_rope_write (rotary embedding, KV write) "
+                            "then mlr_paged_decode"),
             "sclk_mhz": dec["sclk"],
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": ("mlr_paged_decode_append (decode_split_mfma<64,4,false,true>, the "
-                       "split kernel with the KV write folded in, + decode_combine_mfma<64>)"),
+            "kernel": ("mlr_paged_decode_append (decode_mfma<64,4,false,true,true>: 320-token "
+                       "splits, KV write folded in, splits merged in the same launch)"),
             "achieved": round(dec["value_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -725,6 +918,7 @@ def main():
             "avg_launch_us": round(dec["ms_per_step"] * 1e3, 3),
         },
         "cpu_baseline": cpu,
+        "provenance": provenance(),
     }
     if pre is not None:
         line["prefill"] = {
@@ -736,10 +930,16 @@ def main():
                          "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 5),
                          "traffic": traffic["prefill_call_bytes"] if traffic else None},
             "flops_per_call": pre["flops_per_call"],
-            "us_per_call_by_kv_tile": pre["us_per_call"],
-            "sclk_mhz_kv_tile_64": pre["sclk"],
+            "us_per_call": pre["us_per_call"],
+            "us_per_call_min_max": pre["us_per_call_min_max"],
+            "kv_tile": ("the call passes the reference's tile_size 64, which orders the FP32 "
+                        "accumulation only; the kernel steps by its own 64-key tile for "
+                        "any tile_size, so there is one timing, not a tile sweep"),
+            "sclk_mhz": pre["sclk"],
             "cpu_baseline": cpu_pre,
         }
+    line["fp32_decode_b4"] = bench_fp32_decode_b4(
+        device, 0 if args.no_cpu_baseline else args.cpu_budget / 4)
     if not args.no_pre_attention:
         line["pre_attention"] = bench_pre_attention(device)
         line["pre_attention"]["roofline"]["traffic"] = (

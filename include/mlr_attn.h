@@ -195,8 +195,12 @@ int mlr_paged_decode_append_static(
  *
  * Replaces paged_attention_prefill_chunk_tiled
  * (kernels/reference/paged_attention.py:346-434): FP32 online softmax and FP32
- * P@V, output rounded once to the input type. kv_tile selects the key tile the
- * kernel steps by (16, 64 or 128; other values pick the nearest supported).
+ * P@V, output rounded once to the input type. kv_tile is the reference's
+ * tile_size (the key tile of its online-softmax loop, :398-431), which orders
+ * the FP32 accumulation and nothing else; the kernels step by their own key
+ * tile (64 keys on the bf16 matrix-core kernel) whatever kv_tile is, so
+ * results differ from the reference's only by rounding, as they do between
+ * the reference's own tile sizes.
  *   q               : [total_q, num_q_heads, head_dim], strides (q_stride_t, q_stride_h)
  *   block_tables    : int64 [num_seqs, >= max_blocks_per_seq], row stride
  *   query_start_loc : int64 [num_seqs + 1], non-decreasing, starts at 0

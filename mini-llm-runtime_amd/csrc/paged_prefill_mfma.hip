@@ -1,8 +1,8 @@
 // bf16 paged chunk prefill on gfx950 matrix cores (v_mfma_f32_32x32x16_bf16).
 //
 // One workgroup = 128 queries of one query head, four waves of 32 queries.
-// Keys stream through LDS in tiles of BN positions (128 for head_dim 64, 64
-// for head_dim 128) and two stages: while the waves compute on one stage, the
+// Keys stream through LDS in tiles of BN = 64 positions (both head sizes;
+// the launcher fixes it) and two stages: while the waves compute on one stage, the
 // next tile is copied from HBM straight into the other stage with
 // buffer_load_dwordx4 ... lds (no register staging). Each wave copies BN/4
 // consecutive key rows of K and of V, as spans of 16 rows. With block_size a

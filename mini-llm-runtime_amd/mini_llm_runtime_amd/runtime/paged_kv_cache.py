@@ -90,7 +90,8 @@ class PagedKVCache:
     # Token-at-a-time helpers of the reference (:55-176). They address layer 0
     # only, as the reference does, and are not on the serving path.
     # ------------------------------------------------------------------
-    def _get_physical_localtion(self, seq_id, position: int):
+    def _block_and_offset(self, seq_id, position: int):
+        """Physical block and row of a sequence's token position."""
         return (self.block_tables[seq_id][position // self.block_size],
                 position % self.block_size)
 
@@ -105,7 +106,7 @@ class PagedKVCache:
         position = self.seq_lens[seq_id]
         if position // self.block_size == len(self.block_tables[seq_id]):
             self.block_tables[seq_id].append(self._allocate_block())
-        block, offset = self._get_physical_localtion(seq_id, position)
+        block, offset = self._block_and_offset(seq_id, position)
         self.k_cache[0, block, offset].copy_(k)
         self.v_cache[0, block, offset].copy_(v)
         self.seq_lens[seq_id] += 1
@@ -129,7 +130,7 @@ class PagedKVCache:
                             dtype=self.dtype, device=self.device)
         v_out = torch.empty_like(k_out)
         for position in range(seq_len):
-            block, offset = self._get_physical_localtion(seq_id, position)
+            block, offset = self._block_and_offset(seq_id, position)
             k_out[position].copy_(self.k_cache[0, block, offset])
             v_out[position].copy_(self.v_cache[0, block, offset])
         return k_out, v_out
