@@ -1,16 +1,20 @@
 // bf16 paged chunk prefill on gfx950 matrix cores (v_mfma_f32_32x32x16_bf16).
 //
-// One workgroup = 128 queries of one query head, four waves of 32 queries.
+// One workgroup = 128 queries of one query head and eight waves: two splits
+// of the key range (waves 0-3 and 4-7, merged through LDS at the end), each
+// with four waves of 32 queries. Waves w and w + 4 share a SIMD, and the two
+// splits run a ping-pong schedule on it (see the main loop): while one
+// split's waves work the matrix cores, the other's run the softmax on the
+// VALU.
 // Keys stream through LDS in tiles of BN = 64 positions (both head sizes;
-// the launcher fixes it) and two stages: while the waves compute on one stage, the
-// next tile is copied from HBM straight into the other stage with
-// buffer_load_dwordx4 ... lds (no register staging). Each wave copies BN/4
-// consecutive key rows of K and of V, as spans of 16 rows. With block_size a
-// power of two >= 16 a span sits in one cache block, so its source address is
-// scalar (block id and slot base, in a buffer resource) plus a lane-constant
-// offset. Rows past the last key the workgroup needs, and the spans of
-// out-of-range blocks, fall outside the buffer resource and read as zeros;
-// keys of an out-of-range block are also masked.
+// the launcher fixes it), two K and two V stages per split, copied from HBM
+// straight into LDS with buffer_load_dwordx4 ... lds (no register staging),
+// two phases ahead of their use. Each wave copies 16 consecutive key rows of
+// K and of V per tile. With block_size a power of two >= 16 those rows sit in
+// one cache block, so their source address is scalar (a buffer resource at
+// the slot base) plus a lane-constant offset. Rows past the last key the
+// workgroup needs, and out-of-range blocks, fall outside the buffer resource
+// and read as zeros; keys of an out-of-range block are also masked.
 //
 // LDS rows are unpadded (2*D bytes). The 16-byte chunk c of tile row r is
 // stored at chunk c ^ swz(r), which keeps both the K reads of S^T and the
@@ -65,17 +69,15 @@ constexpr float kFloor = -1.0e30f;  // initial reference point (base 2)
 constexpr int kBM = 128;      // queries per workgroup (4 waves x 32)
 constexpr int kSpanRows = 16; // key rows per copy span
 constexpr int kRankMax = 512; // most work items ranked in the prologue
-constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads zeros
 
 template <int D, int BN>
 struct Cfg {
   static constexpr int kRowB = 2 * D;                        // LDS bytes per key row
   static constexpr int kTileB = BN * kRowB;                  // one K (or V) tile
   static constexpr int kChunks = D / 8;                      // 16-byte chunks per row
-  static constexpr int kSpans = BN / 4 / kSpanRows;          // spans per wave and tile
   static constexpr int kCopies = kSpanRows * kRowB / 1024;   // 1 KB copies per span
   static constexpr int kBlocks = BN / 32;                    // 32-key blocks per tile
-  static_assert(kSpans >= 1 && kSpans <= 2, "tile must hold 4 or 8 spans");
+  static_assert(BN / 4 == kSpanRows, "each wave copies one 16-row span per tile");
 };
 
 // Chunk swizzle (depends on the low four row bits only, so it repeats every
@@ -116,10 +118,6 @@ __device__ __forceinline__ int64_t uniform64(int64_t x) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// KS splits of the workgroup's key range run side by side: waves 4k..4k+3
-// take the k-th contiguous share of the tiles for the same 128 queries, and
-// the splits are merged through LDS at the end. A long sequence's critical path
-// shrinks by KS.
 // Rank (0 = most keys) of the work taken by workgroup b of nwg; see the
 // kernel's prologue.
 __device__ __forceinline__ int workgroup_rank(int b, int nwg, int ncu, int pair_cu) {
@@ -137,17 +135,17 @@ void prefill_mfma(PrefillParams p) {
   constexpr int QS = D / 16;         // 16-dim k-steps of S^T
   constexpr int NB = D / 32;         // 32-dim blocks of O^T
   constexpr int KB = C::kBlocks;     // 32-key blocks per tile
-  constexpr int NSP = C::kSpans;
+  static_assert(KS == 2, "the ping-pong schedule pairs two splits");
   // Per split: two stages of K and of V, each a separate LDS object, so that
-  // reads of one stage need not wait for copies into another.
-  // badkS[k][span] is set when that 16-row span of split k's K tile in stage
-  // S lies in an out-of-range block.
+  // reads of one stage need not wait for copies into another. Byte w of
+  // badkS[k] is set when wave w's 16 rows of split k's K tile in stage S lie
+  // in an out-of-range block (bytes 4l + w hold the same flag, one per lane).
   __shared__ __align__(1024) unsigned char ks0[KS][C::kTileB];
   __shared__ __align__(1024) unsigned char ks1[KS][C::kTileB];
   __shared__ __align__(1024) unsigned char vs0[KS][C::kTileB];
   __shared__ __align__(1024) unsigned char vs1[KS][C::kTileB];
-  __shared__ __align__(8) unsigned char badk0[KS][8];
-  __shared__ __align__(8) unsigned char badk1[KS][8];
+  __shared__ __align__(16) unsigned char badk0[KS][256];
+  __shared__ __align__(16) unsigned char badk1[KS][256];
 
   // Work items are (sequence, query tile) pairs, each run once per query head;
   // a workgroup's rank wr = rank * hq + head, where rank orders the items by
@@ -187,12 +185,16 @@ void prefill_mfma(PrefillParams p) {
       if (r == rank) ranked_item = i;
     }
     __syncthreads();
-    item = ranked_item;
+    item = __builtin_amdgcn_readfirstlane(ranked_item);
   } else {
     item = (rank / nqt) * nqt + (nqt - 1 - rank % nqt);
   }
   const int seq = item / nqt, qt = item % nqt;
-  const SeqRange rg = seq_range(p, seq);
+  SeqRange rg = seq_range(p, seq);
+  // Workgroup-uniform: kept in scalar registers.
+  rg.q0 = uniform64(rg.q0);
+  rg.qlen = uniform64(rg.qlen);
+  rg.prefix = uniform64(rg.prefix);
   const int q0 = qt * kBM;
   if (q0 >= rg.qlen) return;  // uniform
   const int kvh = h / p.group;
@@ -242,83 +244,53 @@ void prefill_mfma(PrefillParams p) {
   // logical chunk pc ^ swz(rr) of source row rr.
   const uint32_t row_bytes = static_cast<uint32_t>(p.hkv) * D * 2;  // slot stride
   uint32_t src_off[C::kCopies];
-  int src_row[C::kCopies];
 #pragma unroll
   for (int i = 0; i < C::kCopies; ++i) {
     const int pos = 64 * i + lane;
     const int rr = pos / C::kChunks, pc = pos % C::kChunks;
-    src_row[i] = rr;
     src_off[i] = rr * row_bytes + ((pc ^ swz<D>(rr)) << 4);
   }
-  const int64_t *bt_row = p.bt + static_cast<int64_t>(seq) * p.bt_stride;
+  // The block table is read-only for the whole launch: read it through the
+  // constant address space, so the wave-uniform lookups are scalar loads.
+  typedef __attribute__((address_space(4))) const int64_t const_i64;
+  const const_i64 *bt_row = (const const_i64 *)p.bt + static_cast<int64_t>(seq) * p.bt_stride;
   const int bs_log2 = p.bs_log2;
   const int bs_mask = (1 << bs_log2) - 1;
-  // First position of span sp of this wave in tile t.
-  auto span_pos = [&](int t, int sp) __attribute__((always_inline)) -> int {
-    return t * BN + (BN / 4) * w + kSpanRows * sp;
-  };
-  // Block ids of the wave's spans in tile t (the same in every lane); the
-  // lookup is clamped into the table.
-  auto block_ids = [&](int t, int64_t (&ids)[NSP]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int sp = 0; sp < NSP; ++sp)
-      ids[sp] = bt_row[min(span_pos(t, sp), kv_end - 1) >> bs_log2];
-  };
-  // Copies the wave's spans of tile t from `cache` into the LDS tile `dst`;
-  // with `bad`, also records which spans lie in out-of-range blocks.
-  auto issue = [&](int t, const int64_t (&ids)[NSP], const void *cache, unsigned char *dst,
-                   unsigned char *bad) __attribute__((always_inline)) {
-#pragma unroll
-    for (int sp = 0; sp < NSP; ++sp) {
-      const int pos0 = span_pos(t, sp);
-      const int64_t blk = uniform64(ids[sp]);
-      const bool live = pos0 < kv_end;
-      const bool ok = live && blk >= 0 && blk < p.num_blocks;
-      const int64_t slot = ok ? (blk << bs_log2) + (pos0 & bs_mask) : 0;
-      const int64_t byte0 = (slot * p.hkv + kvh) * (2 * D);
-      const uint32_t nrec = ok ? 15u * row_bytes + 2u * D : 0u;
-      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<unsigned char *>(static_cast<const unsigned char *>(cache) + byte0), 0,
-          nrec, 0x00020000);
-      const int nrows = kv_end - pos0;  // rows of the span that are needed
-      unsigned char *sdst = dst + ((BN / 4) * w + kSpanRows * sp) * C::kRowB;
-#pragma unroll
-      for (int i = 0; i < C::kCopies; ++i) {
-        const uint32_t off = src_row[i] < nrows ? src_off[i] : kOutOfRange;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(sdst + 1024 * i), 16, off,
-                                                 0, 0, 0);
-      }
-      if (bad != nullptr && lane == 0) bad[NSP * w + sp] = (live && !ok) ? 1 : 0;
-    }
-  };
-  auto read_bad = [&](const unsigned char *bad) __attribute__((always_inline)) -> uint64_t {
-    if constexpr (NSP == 2) {
-      const uint2 b = *reinterpret_cast<const uint2 *>(bad);
-      return (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(b.y)) << 32) |
-             __builtin_amdgcn_readfirstlane(b.x);
-    } else {
-      return __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(bad));
-    }
+  // The four waves' out-of-range flags of a K stage (bytes 0..3).
+  auto read_bad = [&](const unsigned char *bad) __attribute__((always_inline)) -> uint32_t {
+    return __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(bad));
   };
 
   // Lane-constant LDS offsets. K read of step st: row m32 (+32 per key block),
   // logical chunk 2st + hh. V^T read (two per MFMA, rows +8 apart): in each
   // 16-lane group G, lane li points at row 4(G/2) + li/4 (+ 16kb) and byte
-  // 64n + 32(G%2) + 8(li%4).
-  int koff[QS];
-#pragma unroll
-  for (int st = 0; st < QS; ++st)
-    koff[st] = m32 * C::kRowB + (((2 * st + hh) ^ swz<D>(m32)) << 4);
+  // 64n + 32(G%2) + 8(li%4). Only the step-0 and (half 0, n 0) offsets are
+  // kept: the swizzle is an XOR of the chunk index, whose parts 2st, 4n lie
+  // in bits of their own, and 8 rows further it flips chunk bit 0, so
+  //   koff(st) = koff0 ^ (st << 5),
+  //   voff(half, n) = (voff0 ^ (half << 4) ^ (n << 6)) + half * 8 rows.
+  const int koff0 = m32 * C::kRowB + ((hh ^ swz<D>(m32)) << 4);
   const int G = lane >> 4, li = lane & 15;
-  int voff[2][NB];
+  const int vrow0 = 4 * (G >> 1) + (li >> 2);
+  const int vbyte0 = 32 * (G & 1) + 8 * (li & 3);
+  const int voff0 =
+      vrow0 * C::kRowB + ((((vbyte0 >> 4) ^ swz<D>(vrow0)) << 4) | (vbyte0 & 15));
+  // The derived offsets are recomputed where they are used (a few XORs)
+  // rather than held in registers across the loop.
+  auto koffs = [&](int (&ko)[QS]) __attribute__((always_inline)) {
+    int k0 = koff0;
+    asm volatile("" : "+v"(k0));
 #pragma unroll
-  for (int half = 0; half < 2; ++half)
+    for (int st = 0; st < QS; ++st) ko[st] = k0 ^ (st << 5);
+  };
+  auto voffs = [&](int (&vo)[2][NB]) __attribute__((always_inline)) {
+    int v0 = voff0;
+    asm volatile("" : "+v"(v0));
 #pragma unroll
-    for (int n = 0; n < NB; ++n) {
-      const int row = 4 * (G >> 1) + (li >> 2) + 8 * half;
-      const int byte = 64 * n + 32 * (G & 1) + 8 * (li & 3);
-      voff[half][n] = row * C::kRowB + ((((byte >> 4) ^ swz<D>(row)) << 4) | (byte & 15));
-    }
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int n = 0; n < NB; ++n) vo[half][n] = (v0 ^ (half << 4) ^ (n << 6)) + half * 8 * C::kRowB;
+  };
 
   // Reference point m of the running softmax (base 2). It stays at the
   // finite floor kFloor (never -inf: a query can see no key at all in one
@@ -338,6 +310,8 @@ void prefill_mfma(PrefillParams p) {
 
   // S^T of one tile from its K stage.
   auto scores = [&](const unsigned char *kst, f32x16_t (&s)[KB]) __attribute__((always_inline)) {
+    int koff[QS];
+    koffs(koff);
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
 #pragma unroll
@@ -347,17 +321,28 @@ void prefill_mfma(PrefillParams p) {
         s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[st], st == 0 ? negm : s[j], 0, 0, 0);
       }
     }
+    // At most two K reads ahead of the MFMAs (four VGPRs each): hoisting all
+    // of them would hold 8 * 4 more registers at the peak of the phase.
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int g = 0; g < KB * QS - 2; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
   // Causal mask (key position <= query position) and out-of-range spans.
-  auto mask = [&](int t, uint64_t badw, f32x16_t (&s)[KB]) __attribute__((always_inline)) {
-    const int lim = qpos - t * BN;  // last visible key of the lane's query
+  // Element i of block j holds key 32j + 8(i/4) + 4hh + i%4, compared here
+  // as the constant 32j + 8(i/4) + i%4 against lim - 4hh; its 16-row span is
+  // 2j + i/8 in every lane.
+  auto mask = [&](int t, uint32_t badw, f32x16_t (&s)[KB]) __attribute__((always_inline)) {
+    const int lim = qpos - t * BN - 4 * hh;  // last visible key of the lane's query
 #pragma unroll
     for (int j = 0; j < KB; ++j)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int key = 32 * j + 8 * (i >> 2) + 4 * hh + (i & 3);
-        const bool dead = key > lim || ((badw >> (8 * (key >> 4))) & 1);
-        if (dead) s[j][i] = -INFINITY;
+        const bool bad = (badw >> (8 * (2 * j + (i >> 3)))) & 1;
+        if (bad || 32 * j + 8 * (i >> 2) + (i & 3) > lim) s[j][i] = -INFINITY;
       }
   };
   // Row max of a tile relative to m (base 2): chains of eight, then the lane pair.
@@ -400,26 +385,97 @@ void prefill_mfma(PrefillParams p) {
         for (int i = 0; i < 16; ++i) s[j][i] -= shift;
     }
   };
-  // P = exp2(S^T) packed to bf16, FP32 row sums (four chains; FP32 adds issue
-  // alongside the MFMAs, v_dot2 would not), and O^T += V^T P^T.
-  auto attend = [&](const f32x16_t (&s)[KB], const unsigned char *vst) __attribute__((always_inline)) {
-    float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+  constexpr int kBatchCopies = 2 * C::kCopies;
+  // s_waitcnt vmcnt(kBatchCopies) lgkmcnt(0), and lgkmcnt(0) alone (gfx9
+  // encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+  constexpr int kWaitBatch = (kBatchCopies & 15) | ((kBatchCopies >> 4) << 14) | 0x70;
+  constexpr int kWaitLds = 0xC07F;
+  const int nw = max(0, min(t_hi, wave_tiles) - t_lo);  // tiles this wave computes
+  // Launches with num_blocks < 2^31 and blocks < 2^31 bytes only.
+  const uint32_t nb32 = static_cast<uint32_t>(p.num_blocks);
+  const uint32_t block_bytes = row_bytes << bs_log2;
+  const uint32_t kv_bytes = static_cast<uint32_t>(kvh) * (2 * D);
+
+  // The wave's span of tile t: the byte offset and record count of a buffer
+  // resource covering the rows the workgroup needs (rows past them, and a
+  // block id out of range, read as zeros) and whether its block id is out
+  // of range. Scalar code, run in the M phase ahead of the V phase that
+  // issues the copies.
+  struct Span {
+    uint32_t off_lo, off_hi, nrec, bad;
+  };
+  auto span_of = [&](int t, int64_t id) __attribute__((always_inline)) -> Span {
+    const int pos0 = t * BN + (BN / 4) * w;
+    const bool live = pos0 < kv_end && t < t_hi;
+    const uint32_t lo = static_cast<uint32_t>(id);
+    const bool ok = live && static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32) == 0 && lo < nb32;
+    const uint32_t nrows = static_cast<uint32_t>(min(kv_end - pos0, kSpanRows));
+    Span sp;
+    sp.nrec = ok ? (nrows - 1) * row_bytes + 2 * D : 0u;
+    const uint64_t byte0 = static_cast<uint64_t>(ok ? lo : 0u) * block_bytes +
+                           static_cast<uint32_t>(pos0 & bs_mask) * row_bytes + kv_bytes;
+    sp.off_lo = static_cast<uint32_t>(byte0);
+    sp.off_hi = static_cast<uint32_t>(byte0 >> 32);
+    sp.bad = (live && !ok) ? 1u : 0u;
+    // Keeps the arithmetic here rather than sunk into the V phase.
+    asm volatile("" : "+s"(sp.off_lo), "+s"(sp.off_hi), "+s"(sp.nrec));
+    return sp;
+  };
+  auto id_of = [&](int t) __attribute__((always_inline)) -> int64_t {
+    return bt_row[min(t * BN + (BN / 4) * w, kv_end - 1) >> bs_log2];
+  };
+  // Copies the wave's 16 rows; with `bad`, records the span's flag there
+  // (lane l writes byte 4l + w, so bytes 0..3 hold the four waves' flags).
+  auto issue_span = [&](const Span &sp, const void *cache, unsigned char *dst,
+                        unsigned char *bad) __attribute__((always_inline)) {
+    const uint64_t byte0 = (static_cast<uint64_t>(sp.off_hi) << 32) | sp.off_lo;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char *>(static_cast<const unsigned char *>(cache) + byte0), 0,
+        sp.nrec, 0x00020000);
+    unsigned char *sdst = dst + (BN / 4) * w * C::kRowB;
 #pragma unroll
-    for (int j = 0; j < KB; ++j) {
-      uint32_t pk[8];
+    for (int i = 0; i < C::kCopies; ++i) {
+      // A local copy: an element of the captured array as the builtin's
+      // argument makes the host pass drop the kernel's launch stub.
+      const uint32_t off = src_off[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(sdst + 1024 * i), 16, off, 0,
+                                               0, 0);
+    }
+    if (bad != nullptr) bad[4 * lane + w] = static_cast<unsigned char>(sp.bad);
+  };
+  // exp2 of a tile's S^T packed to bf16 (the P@V operand), with the FP32
+  // probabilities added to the row sum (four chains).
+  auto probs = [&](const f32x16_t (&sc)[KB], uint32_t (&pk)[KB][8]) __attribute__((always_inline)) {
+    float lsum[4];
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
-        const float p0 = __builtin_amdgcn_exp2f(s[j][2 * x]);
-        const float p1 = __builtin_amdgcn_exp2f(s[j][2 * x + 1]);
-        pk[x] = bf16_pack2(p0, p1);
-        lsum[(2 * x) & 3] += p0;
-        lsum[(2 * x + 1) & 3] += p1;
+        const float p0 = __builtin_amdgcn_exp2f(sc[j][2 * x]);
+        const float p1 = __builtin_amdgcn_exp2f(sc[j][2 * x + 1]);
+        pk[j][x] = bf16_pack2(p0, p1);
+        if (j == 0 && x < 2) {
+          lsum[2 * x] = p0;
+          lsum[2 * x + 1] = p1;
+        } else {
+          lsum[(2 * x) & 3] += p0;
+          lsum[(2 * x + 1) & 3] += p1;
+        }
       }
+    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+  };
+  // O^T += V^T P^T from packed P.
+  auto pv = [&](const uint32_t (&pk)[KB][8], const unsigned char *vst) __attribute__((always_inline)) {
+    int voff[2][NB];
+    voffs(voff);
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
 #pragma unroll
       for (int h16 = 0; h16 < 2; ++h16) {
         const int kb = 2 * j + h16;  // 16-key block
         const bf16x8_t pb = __builtin_bit_cast(
-            bf16x8_t, make_uint4(pk[4 * h16], pk[4 * h16 + 1], pk[4 * h16 + 2], pk[4 * h16 + 3]));
+            bf16x8_t, make_uint4(pk[j][4 * h16], pk[j][4 * h16 + 1], pk[j][4 * h16 + 2],
+                                 pk[j][4 * h16 + 3]));
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
           const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -431,44 +487,112 @@ void prefill_mfma(PrefillParams p) {
           acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[n], 0, 0, 0);
         }
       }
+    // Two MFMAs' V^T reads (two each) ahead of the MFMAs.
+    constexpr int kMfma = 2 * KB * NB;
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int g = 0; g < kMfma - 2; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
 
-  // Pipeline: block ids two tiles ahead, copies one tile ahead; the barrier
-  // after each step (which waits for this wave's copies) publishes the next
-  // stage. The loop is unrolled by two so each stage is a fixed LDS object.
-  // All splits run the same number of steps (an exhausted split idles).
-  int64_t ids[NSP], ids_next[NSP];
-  block_ids(t_lo, ids);
-  block_ids(t_lo + 1, ids_next);
-  if (t_lo < t_hi) {
-    issue(t_lo, ids, p.kc, ks0[split], badk0[split]);
-    issue(t_lo, ids, p.vc, vs0[split], nullptr);
+  // Main loop: a ping-pong schedule of the two key-range splits (waves w and
+  // w + 4 share a SIMD). Per split-local tile i a wave runs an MFMA phase M_i and a
+  // softmax phase V_i, with a workgroup barrier after each phase:
+  //   M_i: O^T += V^T P^T of tile i - 1, S^T of tile i, and the scalar
+  //        set-up of the copies V_i will issue;
+  //   V_i: issue those copies, then mask, row max, rescale, exp2 and bf16
+  //        packing of tile i, with the FP32 row sums.
+  // Split 1 passes one extra barrier first, so it runs a phase behind split
+  // 0 and on every SIMD one wave's matrix-core work overlaps the other's
+  // VALU work:
+  //   phase      0   1   2   3   4  ...
+  //   split 0    M0  V0  M1  V1  M2 ...
+  //   split 1    -   M0  V0  M1  V1 ...
+  // Copies run two phases ahead: V_i copies K(i+2) into K stage i%2 (free
+  // since M_i) and V(i+1) into V stage (i+1)%2 (free since P@V(i-1) in M_i);
+  // M_i needs K(i) and V(i-1), copied in V_{i-2}. Each V phase issues the
+  // same number of copies (tiles past the split read zeros), so before the
+  // barrier ahead of an M phase a wave waits for all but its newest batch.
+  //
+  // Block ids: id_a of tile i + 1 and id_b of tile i + 2 when M_i starts.
+  int64_t id_a, id_b;
+  {
+    const int64_t id0 = id_of(t_lo);
+    id_a = id_of(t_lo + 1);
+    id_b = id_of(t_lo + 2);
+    const Span s0 = span_of(t_lo, id0);
+    issue_span(s0, p.kc, ks0[split], badk0[split]);
+    issue_span(s0, p.vc, vs0[split], nullptr);
+    issue_span(span_of(t_lo + 1, id_a), p.kc, ks1[split], badk1[split]);
   }
-  __syncthreads();
-  auto step = [&](auto stage, int t) __attribute__((always_inline)) {
-    constexpr bool kEven = decltype(stage)::value == 0;
-    if (t + 1 < t_hi) {
-      issue(t + 1, ids_next, p.kc, kEven ? ks1[split] : ks0[split],
-            kEven ? badk1[split] : badk0[split]);
-      issue(t + 1, ids_next, p.vc, kEven ? vs1[split] : vs0[split], nullptr);
-      if (t + 2 < t_hi) block_ids(t + 2, ids_next);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's prologue copies and flags
+  __builtin_amdgcn_s_barrier();
+  if (split == 1) __builtin_amdgcn_s_barrier();
+  // S^T (M to V) and packed P (V to M) are defined in every phase, idle
+  // ones included, so neither is live across the phase that does not use it.
+  f32x16_t s[KB];
+  uint32_t pk[KB][8];
+  uint32_t badw = 0;
+  Span dk, dv;  // copies of the next V phase
+  // M_i: K stage kst holds K(i) and its out-of-range flags kbad (read here:
+  // V_i overwrites them), V stage vst holds V(i-1).
+  auto m_phase = [&](int i, const unsigned char *kst, const unsigned char *kbad,
+                     const unsigned char *vst) __attribute__((always_inline)) {
+    const int64_t id_c = id_of(t_lo + i + 3);  // scalar load, used by M_{i+1}
+    if (i >= 1 && i - 1 < nw) pv(pk, vst);
+    // P dies with the last P@V MFMA before S^T is allocated.
+    __builtin_amdgcn_sched_barrier(0);
+    if (i < nw) {
+      scores(kst, s);
+      badw = read_bad(kbad);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KB; ++j) s[j] = f32x16_t{};
     }
-    if (t < wave_tiles) {
-      f32x16_t s[KB];
-      scores(kEven ? ks0[split] : ks1[split], s);
-      const uint64_t badw = read_bad(kEven ? badk0[split] : badk1[split]);
+    dk = span_of(t_lo + i + 2, id_b);
+    dv = span_of(t_lo + i + 1, id_a);
+    id_a = id_b;
+    id_b = id_c;
+    __builtin_amdgcn_s_waitcnt(kWaitLds);
+    __builtin_amdgcn_s_barrier();
+  };
+  // V_i: copies K(i+2) -> kdst (flags kbad) and V(i+1) -> vdst, then the
+  // softmax of tile i.
+  auto v_phase = [&](int i, unsigned char *kdst, unsigned char *kbad, unsigned char *vdst)
+      __attribute__((always_inline)) {
+    issue_span(dk, p.kc, kdst, kbad);
+    issue_span(dv, p.vc, vdst, nullptr);
+    if (i < nw) {
+      const int t = t_lo + i;
       if (t >= wave_nfull || badw != 0) mask(t, badw, s);
       rescale(tile_max(s), s);
-      attend(s, kEven ? vs0[split] : vs1[split]);
+      probs(s, pk);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+#pragma unroll
+        for (int x = 0; x < 8; ++x) pk[j][x] = 0;
     }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(kWaitBatch);
+    __builtin_amdgcn_s_barrier();
   };
-  for (int s = 0; s < chunk; s += 2) {
-    step(std::integral_constant<int, 0>{}, t_lo + s);
-    if (s + 1 < chunk) step(std::integral_constant<int, 1>{}, t_lo + s + 1);
+  // Unrolled by two so every stage is a fixed LDS object.
+  for (int i = 0; i < chunk; i += 2) {
+    m_phase(i, ks0[split], badk0[split], vs1[split]);
+    v_phase(i, ks0[split], badk0[split], vs1[split]);
+    m_phase(i + 1, ks1[split], badk1[split], vs0[split]);
+    v_phase(i + 1, ks1[split], badk1[split], vs0[split]);
   }
+  // P@V of the last tile when chunk is even (odd chunks ran it above).
+  if ((chunk & 1) == 0) m_phase(chunk, ks0[split], badk0[split], vs1[split]);
+  if (split == 0) __builtin_amdgcn_s_barrier();
+  // Outstanding copies (all of absent tiles) would land on the merge
+  // buffers laid over the stage objects.
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
 
   if constexpr (KS > 1) {
     // Splits 1.. hand (m, l, O^T) to split 0 through LDS, in a lane-major
@@ -570,10 +694,12 @@ bool prefill_mfma_eligible(const PrefillParams &p, int dtype) {
                        (reinterpret_cast<uintptr_t>(p.out) & 7u) == 0 &&
                        p.q_st % 8 == 0 && p.q_sh % 8 == 0 && p.o_st % 4 == 0 &&
                        p.o_sh % 4 == 0;
-  // Positions are 32-bit inside the kernel; a 16-row span must fit a block.
+  // Positions, block ids and in-block byte offsets are 32-bit inside the
+  // kernel; a 16-row span must fit a block.
+  constexpr int64_t k2g = int64_t(1) << 31;
   return dtype == MLR_DTYPE_BF16 && (p.d == 64 || p.d == 128) && aligned &&
-         p.bs_log2 >= 4 && p.max_blocks * p.block_size < (int64_t(1) << 31) &&
-         p.scale > 0.0 && p.scale < 1e30;
+         p.bs_log2 >= 4 && p.max_blocks * p.block_size < k2g && p.num_blocks < k2g &&
+         p.block_size * p.hkv * p.d * 2 < k2g && p.scale > 0.0 && p.scale < 1e30;
 }
 
 int launch_prefill_mfma(const PrefillParams &p, int64_t max_query_len,
