@@ -28,6 +28,8 @@ the decode step above, fp32_decode_b4 (FP32, batch 4), and the chunk prefill.
 Secondary objects: BF16 chunk prefill (8 x 512-token chunks on prefixes
 U[0, 3584]) in TFLOP/s against the 2.5 PFLOP/s bf16 MFMA peak; the decode
 pair the serving runtime runs (fused pre-attention kernel, then decode); the
+read floor of the decode step (config.read_floor: a read-only pass over the
+same K/V rows through the same block tables, mlr_paged_kv_read_floor); the
 8 x 32K decode over rotated pools; the fused pre-attention step; and
 ``serving``, end-to-end continuous-batching steps of a random-init
 Qwen2.5-0.5B-shape model in BF16 (workloads.qwen05b_serving: about 48
@@ -190,8 +192,12 @@ def profile_run(args, device):
         k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
         kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, workspace=ws, new_k=new_k,
                                 new_v=new_v, slot_mapping=slots)
+    floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // 320), dtype=torch.int32, device=device)
+    for i in range(LAYERS):
+        k_layer, v_layer = cache.get_layer_cache(i)
+        kpa.paged_kv_read_floor(k_layer, v_layer, bt, ctx, tokens_per_item=320, out=floor_out)
     torch.cuda.synchronize()
-    print(f"profile: {args.steps} decode steps", flush=True)
+    print(f"profile: {args.steps} decode steps, {LAYERS} read-floor passes", flush=True)
     del cache
     if not args.no_prefill:
         pw = workloads.bf16_prefill_chunk512_x8()
@@ -286,6 +292,9 @@ def bench_decode(args, device):
     positions = (ctx - 1).contiguous()
     inv_freq = Qwen2RotaryEmbedding(64, 1_000_000.0).inv_freq.to(device)
     q_rot = torch.empty_like(q)
+    floor_items = (64, 96, 160, 320)
+    floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // min(floor_items)), dtype=torch.int32,
+                            device=device)
 
     def step(layer, kind="step"):
         k_layer, v_layer = cache.get_layer_cache(layer)
@@ -296,6 +305,9 @@ def bench_decode(args, device):
         elif kind == "decode":  # decode only
             kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out,
                                     tokens_per_split=ts, workspace=workspace)
+        elif kind.startswith("floor"):  # read-only pass over the same K/V rows
+            kpa.paged_kv_read_floor(k_layer, v_layer, bt, ctx,
+                                    tokens_per_item=int(kind[5:]), out=floor_out)
         else:                   # served pair
             kpre.qkv_rope_write(qkv, positions, inv_freq, cache, layer, slots, 14, out=q_rot)
             kpa.paged_decode_launch(q_rot, k_layer, v_layer, bt, ctx, out,
@@ -326,7 +338,8 @@ def bench_decode(args, device):
     t_step = timed_graph(g_steps, 1, stream)
     # A larger sample of the same graph (10 replays) as a cross-check.
     t_step10 = timed_graph(g_steps, 10, stream) / 10
-    graphs = {kind: capture(kind, LAYERS) for kind in ("decode", "served")}
+    graphs = {kind: capture(kind, LAYERS)
+              for kind in ("decode", "served", *(f"floor{n}" for n in floor_items))}
     res = {}
     for kind, g in graphs.items():
         warm_graph(g, stream)
@@ -335,6 +348,21 @@ def bench_decode(args, device):
     decode_bytes = wl.algorithmic_bytes()
     step_bytes = decode_bytes + wl.write_bytes()
     sec_per_step = t_step / steps
+    # The read floor: every context token's K and V rows read through the
+    # same block tables (mlr_paged_kv_read_floor), no compute, best item size.
+    kv_bytes = int(wl.context_lens.sum()) * 2 * 2 * 64 * 2
+    floor_us = {n: res[f"floor{n}"] * 1e6 for n in floor_items}
+    best = min(floor_us, key=floor_us.get)
+    read_floor = {
+        "kernel": "mlr_paged_kv_read_floor (kv_read_floor_kernel): read-only pass over the "
+                  "step's K/V rows through the same block tables, XOR checksum",
+        "kv_bytes": kv_bytes,
+        "us_by_tokens_per_item": {str(n): round(v, 3) for n, v in floor_us.items()},
+        "us": round(floor_us[best], 3),
+        "GBps": round(kv_bytes / (floor_us[best] * 1e-6) / 1e9, 1),
+        "frac_of_hbm_peak": round(kv_bytes / (floor_us[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "step_us_over_floor_us": round(sec_per_step * 1e6 / floor_us[best], 3),
+    }
     return {
         "wl": wl,
         "steps": steps,
@@ -345,6 +373,7 @@ def bench_decode(args, device):
         "decode_us": res["decode"] * 1e6,
         "decode_gbs": decode_bytes / res["decode"] / 1e9,
         "served_us": res["served"] * 1e6,
+        "read_floor": read_floor,
         "decode_bytes": decode_bytes,
         "step_bytes": step_bytes,
         "stream": stream,
@@ -902,6 +931,7 @@ def main():
             "served_step": ("what Qwen2Attention.forward_decode_batch_with_cache runs after "
                             "its QKV GEMM: mlr_qkv_rope_write (rotary embedding, KV write) "
                             "then mlr_paged_decode"),
+            "read_floor": dec["read_floor"],
             "sclk_mhz": dec["sclk"],
         },
         "roofline": {
@@ -945,6 +975,7 @@ def main():
         line["pre_attention"]["roofline"]["traffic"] = (
             traffic.get("pre_attention_call_bytes") if traffic else None)
     line["decode_32k"] = bench_decode_32k(device)
+    line["decode_32k"]["traffic"] = traffic.get("decode_32k_bytes") if traffic else None
     line["accumulator"] = bench_accumulator(device)
     if not args.no_serving:
         line["serving"] = bench_serving(device)

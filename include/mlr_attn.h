@@ -305,6 +305,29 @@ int mlr_build_step_metadata(const int64_t *req_info, const int64_t *block_tables
                             int64_t *slot_mapping, int64_t *query_start_loc,
                             int64_t *context_lens, void *stream);
 
+/*
+ * Diagnostics. No counterpart in the reference: a read-only pass that
+ * measures the memory floor of a decode step on its own block list.
+ *
+ * mlr_paged_kv_read_floor reads, for every sequence b < batch and every
+ * context token t < context_lens[b] (clamped to max_blocks * block_size),
+ * the whole slot row (row_bytes = Hkv * D * element size, a multiple of 16)
+ * of K and of V through block_tables, and XOR-folds every 32-bit word of
+ * those rows into out: one word per (sequence, item of tokens_per_item
+ * tokens), out[b * items + i], 0 for items past the context; blocks outside
+ * [0, num_blocks) read as zeros. The XOR of all out words is the XOR of all
+ * the words read. tokens_per_item is a multiple of block_size, at most 512
+ * blocks; block_size is a power of two; out_len >= the count that
+ * mlr_paged_kv_read_floor_outputs returns (0 for invalid sizes).
+ */
+size_t mlr_paged_kv_read_floor_outputs(int64_t batch, int64_t max_blocks, int64_t block_size,
+                                       int64_t tokens_per_item);
+int mlr_paged_kv_read_floor(const void *k_cache, const void *v_cache, int64_t num_blocks,
+                            int64_t block_size, int64_t row_bytes, const int64_t *block_tables,
+                            int64_t bt_stride, int64_t max_blocks, const int64_t *context_lens,
+                            int64_t batch, int64_t tokens_per_item, uint32_t *out,
+                            int64_t out_len, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -452,3 +452,32 @@ def paged_attention_prefill_varlen(
         max_query_len = int(qlens.max().item()) if qlens.numel() else 0
     return paged_prefill_launch(q, k_cache, v_cache, block_tables, query_start_loc,
                                 context_lens, max_query_len, tile_size=tile_size)
+
+
+def paged_kv_read_floor(k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        block_tables: torch.Tensor, context_lens: torch.Tensor,
+                        tokens_per_item: int = 320,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """Diagnostic (no reference counterpart): read every context token's K and
+    V slot row through the block table and return the XOR checksums of the
+    32-bit words read, one int32 per (sequence, item of `tokens_per_item`
+    tokens). The time of this call is the memory floor of a decode step on
+    the same block list. Operands as for paged_decode_launch."""
+    device = _lib.require_hip(k_cache, v_cache, block_tables, context_lens,
+                              what="paged KV read floor")
+    lib = _lib.load()
+    num_blocks, block_size = k_cache.shape[0], k_cache.shape[1]
+    row_bytes = k_cache[0, 0].numel() * k_cache.element_size()
+    block_tables = block_tables.to(torch.long).contiguous()
+    context_lens = context_lens.to(torch.long).contiguous()
+    batch, width = block_tables.shape
+    n = int(lib.mlr_paged_kv_read_floor_outputs(batch, width, block_size, tokens_per_item))
+    if out is None:
+        out = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        status = lib.mlr_paged_kv_read_floor(
+            k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, block_size, row_bytes,
+            block_tables.data_ptr(), block_tables.stride(0), width, context_lens.data_ptr(),
+            batch, tokens_per_item, out.data_ptr(), out.numel(), _lib.stream_handle(device))
+    _lib.check(status, "mlr_paged_kv_read_floor")
+    return out
