@@ -432,13 +432,20 @@ def bench_prefill(device, reps=5, calls_per_graph=10):
     }
 
 
-def bench_pre_attention(device, reps=4, calls_per_graph=10):
+def bench_pre_attention(device, reps=4, calls_per_graph=100):
     """The step before attention at a Qwen2.5-0.5B layer (hidden 896, 14/2
     heads, head_dim 64, BF16) for a decode batch (48 tokens) and a prefill
     step (2048 tokens): the fused mlr_qkv_rope_write kernel alone, the fused
     step (one GEMM over the concatenated projections + the kernel), and the
     reference's unfused sequence (three projection GEMMs, rotary embedding in
-    PyTorch ops, then the KV write)."""
+    PyTorch ops, then the KV write).
+
+    Each figure is the event-timed average over `reps` replays of a graph of
+    `calls_per_graph` calls: long enough that the host's graph launches keep
+    ahead of the GPU (with 10-call graphs they do not, and the per-call time
+    grows by ~2 us). `graph_node_us` is the same measurement for a one-element
+    fill kernel: the per-launch cost a graph node adds, which the `_net`
+    figures subtract."""
     import types
 
     import torch
@@ -465,9 +472,11 @@ def bench_pre_attention(device, reps=4, calls_per_graph=10):
         with torch.cuda.graph(g, stream=stream):
             for _ in range(calls_per_graph):
                 fn()
-        warm_graph(g, stream, seconds=0.1)
+        warm_graph(g, stream, seconds=0.25)
         return timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
 
+    node = torch.zeros(1, device=device)
+    node_us = graph_us(lambda: node.zero_())
     out = {}
     for tokens in (48, 2048):
         gen = torch.Generator().manual_seed(tokens)
@@ -490,14 +499,18 @@ def bench_pre_attention(device, reps=4, calls_per_graph=10):
         k_us = graph_us(kernel)
         out[str(tokens)] = {
             "fused_kernel_us": round(k_us, 3),
+            "fused_kernel_net_us": round(k_us - node_us, 3),
             "fused_step_us": round(graph_us(fused), 3),
             "unfused_step_us": round(graph_us(unfused), 3),
             "kernel_bytes": tokens * bytes_per_token,
             "kernel_GBps": round(tokens * bytes_per_token / k_us / 1e3, 1),
+            "kernel_net_GBps": round(tokens * bytes_per_token / (k_us - node_us) / 1e3, 1),
         }
     big = out["2048"]
     return {
         "workload": "qwen05b_layer_pre_attention_bf16",
+        "calls_per_graph": calls_per_graph,
+        "graph_node_us": round(node_us, 3),
         "by_tokens": out,
         "roofline": {"bound": "hbm", "kernel": "mlr_qkv_rope_write (2048 tokens)",
                      "achieved": big["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -564,7 +577,7 @@ def bench_decode_32k(device, reps=4, calls_per_graph=6):
             "frac_of_hbm_peak_best": round(nbytes / best_us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
-def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=10):
+def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=100):
     """The CUDA accumulator extension's contract (p [B, 64], v [B, 64, 256],
     FP32) on mlr_pa_accumulate at the reference test's largest batch."""
     import torch

@@ -22,6 +22,28 @@ from ..runtime.paged_kv_cache import PagedKVCache
 
 _SUPPORTED = (torch.float32, torch.float16, torch.bfloat16)
 
+# FP32 copies of rotary inv_freq buffers held in another dtype (a model cast
+# to bf16 casts its buffers), so that a call does not launch a conversion.
+# An entry keeps its source tensor alive, so the source's storage cannot be
+# reused while cached, and records the source's version counter, so an
+# in-place change of the buffer is seen.
+_FREQ32: dict = {}
+_FREQ32_MAX = 64
+
+
+def _freq_fp32(inv_freq: torch.Tensor) -> torch.Tensor:
+    if inv_freq.dtype == torch.float32 and inv_freq.is_contiguous():
+        return inv_freq
+    key = (inv_freq.data_ptr(), inv_freq.dtype, inv_freq.device, inv_freq.stride())
+    hit = _FREQ32.get(key)
+    if hit is not None and hit[0] is inv_freq and hit[1] == inv_freq._version:
+        return hit[2]
+    freq = inv_freq.to(torch.float32).contiguous()
+    if len(_FREQ32) >= _FREQ32_MAX:
+        _FREQ32.clear()
+    _FREQ32[key] = (inv_freq, inv_freq._version, freq)
+    return freq
+
 
 def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor,
                    kv_cache: PagedKVCache, layer_idx: int, slot_mapping: torch.Tensor,
@@ -72,7 +94,7 @@ def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, inv_freq: torch.T
     layer_k, layer_v = kv_cache.get_layer_cache(layer_idx)
     if not (layer_k.is_contiguous() and layer_v.is_contiguous()):
         raise ValueError("KV cache layers must be contiguous")
-    freq = inv_freq.to(torch.float32).contiguous()
+    freq = _freq_fp32(inv_freq)
     bias_c = bias.contiguous() if bias is not None else None
     lib = _lib.load()
     with torch.cuda.device(device):

@@ -325,3 +325,19 @@ def test_accumulator_rejects_cpu_tensors(p, v, error, message):
     from mini_llm_runtime_amd.kernels.accumulator import paged_attention_accumulator_cuda
     with pytest.raises(error, match=message):
         paged_attention_accumulator_cuda(p, v)
+
+
+def test_rotary_freq_cache_follows_in_place_changes():
+    # The FP32 copy of a bf16 inv_freq buffer is reused while the buffer is
+    # unchanged and rebuilt after an in-place change.
+    from mini_llm_runtime_amd.kernels import pre_attention as kpre
+
+    f = torch.tensor([1.0, 0.5, 0.25, 0.125], dtype=torch.bfloat16)
+    a = kpre._freq_fp32(f)
+    assert a.dtype == torch.float32 and torch.equal(a, f.float())
+    assert kpre._freq_fp32(f) is a
+    f.mul_(2)
+    b = kpre._freq_fp32(f)
+    assert b is not a and torch.equal(b, f.float())
+    g = torch.tensor([1.0, 0.5], dtype=torch.float32)
+    assert kpre._freq_fp32(g) is g
