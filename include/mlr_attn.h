@@ -89,9 +89,11 @@ int mlr_kv_write(const void *k, const void *v, int src_dtype,
 /*
  * Bytes of workspace mlr_paged_decode needs for these sizes. `max_context`
  * bounds every context length (the host passes block_table width * block_size).
- * tokens_per_split <= 0 sizes for 256-token splits, the smallest split the
- * library picks by default (bf16 head_dim 64/128: max(256, ceil(max_context /
- * 16)) rounded up to a multiple of 256; otherwise 256).
+ * tokens_per_split <= 0 sizes for the library's default splits, whichever
+ * kernel the call takes. The defaults: bf16 head_dim 64/128 (matrix-core
+ * kernel) 320 tokens at head_dim 64 when max_context <= 5120, else
+ * max(256, ceil(max_context / 16)) rounded up to a multiple of 256; other
+ * dtypes and shapes an eighth of max_context as a power of two in [32, 256].
  */
 size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
                                        int64_t head_dim, int64_t max_context,

@@ -92,6 +92,8 @@ __global__ __launch_bounds__(256) void decode_split_generic(DecodeParams p) {
       Acc dot = 0;
       const T *kr = kc + r;
       const Acc *qg = q_s + g * p.d;
+      // Unrolled so that a row's loads are in flight together.
+#pragma unroll 16
       for (int e = 0; e < p.d; ++e) dot += qg[e] * E::to_acc(kr[e]);
       s = decode_score<T>(dot, p.scale);
     }
@@ -119,15 +121,50 @@ __global__ __launch_bounds__(256) void decode_split_generic(DecodeParams p) {
   }
   __syncthreads();
 
+  // P@V: wave w takes the group's heads w, w + nw, ... (up to kGenHeads / 4
+  // of them) and lane l the dimensions l, l + 64, ...; for each token the
+  // wave loads the V row once, coalesced, for all its heads. Each output is
+  // summed by one lane in token order. Tokens go kTok at a time, so kTok rows
+  // are in flight per lane.
+  constexpr int kHpw = kGenHeads / 4;
   Acc *ws_acc = static_cast<Acc *>(p.ws_acc);
-  for (int i = threadIdx.x; i < ng * p.d; i += blockDim.x) {
-    const int g = i / p.d, e = i % p.d;
-    Acc a = 0;
-    for (int t = 0; t < n; ++t) {
-      const int64_t r = row_s[t];
-      if (r >= 0) a += static_cast<Acc>(s_s[g * p.ts + t]) * E::to_acc(vc[r + e]);
+  for (int e = lane; e < p.d; e += kWave) {
+    Acc a[kHpw];
+#pragma unroll
+    for (int j = 0; j < kHpw; ++j) a[j] = 0;
+    constexpr int kTok = 8;
+    int t = 0;
+    for (; t + kTok <= n; t += kTok) {
+      Acc v[kTok];
+      int64_t r[kTok];
+#pragma unroll
+      for (int u = 0; u < kTok; ++u) {
+        r[u] = row_s[t + u];
+        v[u] = r[u] >= 0 ? E::to_acc(vc[r[u] + e]) : Acc(0);
+      }
+#pragma unroll
+      for (int u = 0; u < kTok; ++u)
+#pragma unroll
+        for (int j = 0; j < kHpw; ++j) {
+          const int g = wave + nw * j;
+          if (g < ng && r[u] >= 0) a[j] += static_cast<Acc>(s_s[g * p.ts + t + u]) * v[u];
+        }
     }
-    ws_acc[(((int64_t)b * p.hq + head0 + g) * p.max_splits + split) * p.d + e] = a;
+    for (; t < n; ++t) {
+      const int64_t r = row_s[t];
+      if (r < 0) continue;
+      const Acc v = E::to_acc(vc[r + e]);
+#pragma unroll
+      for (int j = 0; j < kHpw; ++j) {
+        const int g = wave + nw * j;
+        if (g < ng) a[j] += static_cast<Acc>(s_s[g * p.ts + t]) * v;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kHpw; ++j) {
+      const int g = wave + nw * j;
+      if (g < ng) ws_acc[(((int64_t)b * p.hq + head0 + g) * p.max_splits + split) * p.d + e] = a[j];
+    }
   }
 }
 
@@ -218,7 +255,9 @@ int launch_combine(const DecodeParams &p, hipStream_t stream) {
 template int launch_combine<bf16_t>(const DecodeParams &, hipStream_t);
 
 int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_context) {
-  // Generic kernel: 256 tokens, whose scores it holds in LDS. Matrix-core
+  // Generic kernel: an eighth of the longest context, as a power of two in
+  // [32, 256] (its scores are held in LDS), so that short contexts still
+  // spread over several workgroups per (sequence, KV head). Matrix-core
   // kernel at head_dim 64 with contexts of up to 16 x 320 tokens: 320 (four
   // tiles per wave in registers and one in LDS), so a batch of long contexts
   // fits the GPU in one generation of workgroups. Otherwise at least 256
@@ -226,7 +265,11 @@ int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_contex
   // splits per sequence: long contexts then get fewer, longer splits
   // (measured at 8 x 32K tokens: 133 us with 128 splits, 108-111 us with
   // 8-16), and the merge takes every sequence in one 16-split chunk.
-  if (!mfma) return 256;
+  if (!mfma) {
+    int64_t ts = 32;
+    while (ts < 256 && ts * 8 < max_context) ts *= 2;
+    return ts;
+  }
   if (head_dim == 64 && max_context <= 16 * kLdsSplit64) return kLdsSplit64;
   const int64_t per16 = ceil_div(max_context, 16);
   return per16 <= 256 ? 256 : ceil_div(per16, 256) * 256;
@@ -256,10 +299,11 @@ extern "C" size_t mlr_paged_decode_workspace_size(int64_t batch,
                                                   int dtype) {
   if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_context <= 0)
     return 0;
-  // The default is sized for 256-token splits, the most splits either kernel
-  // uses by default, so it covers whichever kernel the call takes.
-  (void)head_dim;
-  const int64_t ts = tokens_per_split > 0 ? tokens_per_split : 256;
+  // The default is sized for the generic kernel's split, the smallest either
+  // kernel uses by default, so it covers whichever kernel the call takes.
+  const int64_t ts = tokens_per_split > 0
+                         ? tokens_per_split
+                         : default_tokens_per_split(false, head_dim, max_context);
   const int64_t splits = ceil_div(max_context, ts);
   return static_cast<size_t>(
       decode_workspace_layout(batch, num_q_heads, head_dim, splits, dtype).total);
