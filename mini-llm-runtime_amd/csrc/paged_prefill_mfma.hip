@@ -404,16 +404,21 @@ void prefill_mfma(PrefillParams p) {
   struct Span {
     uint32_t off_lo, off_hi, nrec, bad;
   };
+  // In-block byte offset of the wave's rows: (64t + 16w) & bs_mask is
+  // ((64t) & bs_mask) + ((16w) & bs_mask), as 64t has no bits below 64 and
+  // 16w < 64; the second part (and the KV head's offset) is per wave.
+  const uint32_t inblk_w = static_cast<uint32_t>((kSpanRows * w) & bs_mask) * row_bytes + kv_bytes;
   auto span_of = [&](int t, int64_t id) __attribute__((always_inline)) -> Span {
     const int pos0 = t * BN + (BN / 4) * w;
     const bool live = pos0 < kv_end && t < t_hi;
     const uint32_t lo = static_cast<uint32_t>(id);
-    const bool ok = live && static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32) == 0 && lo < nb32;
+    const uint32_t hi = static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32);
+    const bool ok = live && hi == 0u && lo < nb32;
     const uint32_t nrows = static_cast<uint32_t>(min(kv_end - pos0, kSpanRows));
     Span sp;
     sp.nrec = ok ? (nrows - 1) * row_bytes + 2 * D : 0u;
     const uint64_t byte0 = static_cast<uint64_t>(ok ? lo : 0u) * block_bytes +
-                           static_cast<uint32_t>(pos0 & bs_mask) * row_bytes + kv_bytes;
+                           (static_cast<uint32_t>((t * BN) & bs_mask) * row_bytes + inblk_w);
     sp.off_lo = static_cast<uint32_t>(byte0);
     sp.off_hi = static_cast<uint32_t>(byte0 >> 32);
     sp.bad = (live && !ok) ? 1u : 0u;
@@ -517,16 +522,20 @@ void prefill_mfma(PrefillParams p) {
   // same number of copies (tiles past the split read zeros), so before the
   // barrier ahead of an M phase a wave waits for all but its newest batch.
   //
-  // Block ids: id_a of tile i + 1 and id_b of tile i + 2 when M_i starts.
-  int64_t id_a, id_b;
+  // dk: the span of the newest K copy issued (tile i + 1 when M_i starts);
+  // the V copy of the same tile, one phase later, reads the same rows of the
+  // V cache. id_b: the block id of tile i + 2 when M_i starts.
+  Span dk, dv;
+  int64_t id_b;
   {
     const int64_t id0 = id_of(t_lo);
-    id_a = id_of(t_lo + 1);
+    const int64_t id1 = id_of(t_lo + 1);
     id_b = id_of(t_lo + 2);
     const Span s0 = span_of(t_lo, id0);
     issue_span(s0, p.kc, ks0[split], badk0[split]);
     issue_span(s0, p.vc, vs0[split], nullptr);
-    issue_span(span_of(t_lo + 1, id_a), p.kc, ks1[split], badk1[split]);
+    dk = span_of(t_lo + 1, id1);
+    issue_span(dk, p.kc, ks1[split], badk1[split]);
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wave's prologue copies and flags
   __builtin_amdgcn_s_barrier();
@@ -536,7 +545,6 @@ void prefill_mfma(PrefillParams p) {
   f32x16_t s[KB];
   uint32_t pk[KB][8];
   uint32_t badw = 0;
-  Span dk, dv;  // copies of the next V phase
   // M_i: K stage kst holds K(i) and its out-of-range flags kbad (read here:
   // V_i overwrites them), V stage vst holds V(i-1).
   auto m_phase = [&](int i, const unsigned char *kst, const unsigned char *kbad,
@@ -552,9 +560,8 @@ void prefill_mfma(PrefillParams p) {
 #pragma unroll
       for (int j = 0; j < KB; ++j) s[j] = f32x16_t{};
     }
+    dv = dk;  // V(i+1) reads the rows K(i+1) read
     dk = span_of(t_lo + i + 2, id_b);
-    dv = span_of(t_lo + i + 1, id_a);
-    id_a = id_b;
     id_b = id_c;
     __builtin_amdgcn_s_waitcnt(kWaitLds);
     __builtin_amdgcn_s_barrier();
