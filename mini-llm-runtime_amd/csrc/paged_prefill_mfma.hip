@@ -550,6 +550,9 @@ void prefill_mfma(PrefillParams p) {
   auto m_phase = [&](int i, const unsigned char *kst, const unsigned char *kbad,
                      const unsigned char *vst) __attribute__((always_inline)) {
     const int64_t id_c = id_of(t_lo + i + 3);  // scalar load, used by M_{i+1}
+    // Raised wave priority for the matrix work: the other split's softmax
+    // phase on this SIMD takes the issue slots the MFMAs leave.
+    __builtin_amdgcn_s_setprio(3);
     if (i >= 1 && i - 1 < nw) pv(pk, vst);
     // P dies with the last P@V MFMA before S^T is allocated.
     __builtin_amdgcn_sched_barrier(0);
@@ -560,6 +563,7 @@ void prefill_mfma(PrefillParams p) {
 #pragma unroll
       for (int j = 0; j < KB; ++j) s[j] = f32x16_t{};
     }
+    __builtin_amdgcn_s_setprio(0);
     dv = dk;  // V(i+1) reads the rows K(i+1) read
     dk = span_of(t_lo + i + 2, id_b);
     id_b = id_c;
