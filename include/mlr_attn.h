@@ -116,12 +116,17 @@ size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
  *   tokens_per_split: split-KV granularity in tokens (<= 0: library default)
  *   workspace    : >= mlr_paged_decode_workspace_size(...) bytes, 256-aligned,
  *                  all-zero before its first use (hipMemset once). It holds
- *                  per-(sequence, KV head) arrival counters that the bf16
- *                  matrix-core kernel uses to merge the splits in one launch
- *                  (the last split of a sequence to finish merges them); every
- *                  call returns them to zero, so the workspace can be reused
- *                  without clearing, including inside captured graphs. Calls
- *                  that share a workspace must not overlap.
+ *                  the splits' partial results; the bf16 matrix-core kernel
+ *                  merges them in the same launch (the workgroup of a
+ *                  sequence's last split waits for the words of the others
+ *                  to arrive, a zero word meaning "not yet"). Every call
+ *                  returns each word it wrote to zero, so the workspace can be
+ *                  reused without clearing, by calls of any shape and inside
+ *                  captured graphs. Calls that share a workspace must not
+ *                  overlap. Should a merge ever wait past its limit (it waits
+ *                  only for workgroups launched before its own), it sets the
+ *                  workspace's first word and writes NaN, and so does every
+ *                  later merge on that workspace until it is zeroed again.
  *   out          : [batch, num_q_heads, head_dim], strides (out_stride_b, out_stride_h)
  */
 int mlr_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -170,8 +175,9 @@ int mlr_paged_decode_append(
  * code under graph capture or a serving loop that forbids allocation.
  *   - Sizes whose scratch would pass 8 MiB are rejected (MLR_ERR_WORKSPACE)
  *     before anything is launched or written; mlr_paged_decode_workspace_size
- *     gives the need (e.g. 64 sequences x 28 query heads x 16 splits of
- *     head_dim 128 fit).
+ *     gives the need (e.g. 64 sequences x 14 query heads x 16 splits of
+ *     head_dim 64 take 3.6 MiB; 64 x 28 x 16 of head_dim 128 would take
+ *     14.2 MiB and is rejected).
  *   - Every call on one GPU shares that GPU's array: calls that overlap on one
  *     GPU (other streams, other threads) race and must not be issued.
  *   - Arguments, results and cache contents are those of

@@ -25,7 +25,9 @@ struct DecodeParams {
   double scale;
   int ts;          // tokens per split
   int max_splits;  // splits covering max_blocks * block_size tokens
-  int *ws_ctr;     // [batch][hkv] arrival counters of the single-launch merge
+  int split_stride;  // workspace rows per (sequence, query head): max_splits
+                     // rounded up to kSplitRowPad
+  uint32_t *ws_flag;  // failure word of the single-launch merge (zero: none)
   float2 *ws_ml;   // [batch][hq][max_splits] = (m, l)
   void *ws_acc;    // [batch][hq][max_splits][d], FP32 (FP64 for f64 inputs)
   int ml_base2;    // 1: m is a base-2 exponent, 0: natural-log units
@@ -40,12 +42,14 @@ struct DecodeParams {
   void *vc_w;
 };
 
-// Workspace: a fixed region of arrival counters (zero between calls), then
-// the split partials (m, l) and acc, each 256-byte aligned. The counter
-// region has the same size for every call, so the partials of one call never
-// land where a later call with another shape keeps its counters.
-constexpr int64_t kCounterSlots = 65536;  // (sequence, KV head) pairs, at most
-constexpr int64_t kCounterBytes = kCounterSlots * 4;
+// Workspace: a 256-byte flag region, then the split partials (m, l) and acc,
+// each 256-byte aligned. Every byte of it is zero between calls: each call
+// returns the partial rows it wrote to zero once they are merged, whatever
+// kernel wrote them, so calls of any shape can share one workspace.
+constexpr int64_t kFlagBytes = 256;
+// Rows per (sequence, query head) come in multiples of this, so the merge can
+// read 16 consecutive split rows of one head without leaving that head's rows.
+constexpr int64_t kSplitRowPad = 16;
 struct DecodeWorkspace {
   int64_t ml_offset;
   int64_t acc_offset;

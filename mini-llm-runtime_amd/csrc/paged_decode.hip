@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void decode_split_generic(DecodeParams p) {
     }
     l = wave_sum(l);
     if (lane == 0) {
-      p.ws_ml[((int64_t)b * p.hq + head0 + g) * p.max_splits + split] =
+      p.ws_ml[((int64_t)b * p.hq + head0 + g) * p.split_stride + split] =
           make_float2(m, l);
     }
   }
@@ -163,12 +163,14 @@ __global__ __launch_bounds__(256) void decode_split_generic(DecodeParams p) {
 #pragma unroll
     for (int j = 0; j < kHpw; ++j) {
       const int g = wave + nw * j;
-      if (g < ng) ws_acc[(((int64_t)b * p.hq + head0 + g) * p.max_splits + split) * p.d + e] = a[j];
+      if (g < ng) ws_acc[(((int64_t)b * p.hq + head0 + g) * p.split_stride + split) * p.d + e] = a[j];
     }
   }
 }
 
-// Pass 2 for every path: one workgroup per (query head, sequence).
+// Pass 2 of the generic path: one workgroup per (query head, sequence). Each
+// thread returns the partial words it read to zero (no other thread reads
+// them), so the workspace is all zero again when the call ends.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
   using E = Elem<T>;
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
   int64_t ctx = p.ctx[b];
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int ns = static_cast<int>(ceil_div(ctx, p.ts));
-  const float2 *ml = p.ws_ml + ((int64_t)b * p.hq + h) * p.max_splits;
+  float2 *ml = p.ws_ml + ((int64_t)b * p.hq + h) * p.split_stride;
 
   extern __shared__ __align__(16) unsigned char smem[];
   float *w_s = reinterpret_cast<float *>(smem);  // [max_splits]
@@ -206,6 +208,7 @@ __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
                                       : expf(v.x - M);
     w_s[s] = w;
     l += w * v.y;
+    ml[s] = make_float2(0.f, 0.f);
   }
   l = wave_sum(l);
   __syncthreads();
@@ -219,12 +222,14 @@ __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
   __syncthreads();
   const float L = red[1];
 
-  const Acc *acc = static_cast<const Acc *>(p.ws_acc) +
-                   ((int64_t)b * p.hq + h) * p.max_splits * p.d;
+  Acc *acc = static_cast<Acc *>(p.ws_acc) + ((int64_t)b * p.hq + h) * p.split_stride * p.d;
   T *out = static_cast<T *>(p.out) + b * p.o_sb + h * p.o_sh;
   for (int e = threadIdx.x; e < p.d; e += blockDim.x) {
     Acc a = 0;
-    for (int s = 0; s < ns; ++s) a += static_cast<Acc>(w_s[s]) * acc[(int64_t)s * p.d + e];
+    for (int s = 0; s < ns; ++s) {
+      a += static_cast<Acc>(w_s[s]) * acc[(int64_t)s * p.d + e];
+      acc[(int64_t)s * p.d + e] = Acc(0);
+    }
     out[e] = E::from_acc(a / static_cast<Acc>(L));
   }
 }
@@ -278,8 +283,8 @@ int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_contex
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype) {
   DecodeWorkspace w;
-  w.ml_offset = kCounterBytes;
-  const int64_t rows = batch * hq * max_splits;
+  w.ml_offset = kFlagBytes;
+  const int64_t rows = batch * hq * (ceil_div(max_splits, kSplitRowPad) * kSplitRowPad);
   const int64_t ml_bytes = rows * static_cast<int64_t>(sizeof(float2));
   w.acc_offset = w.ml_offset + (ml_bytes + 255) / 256 * 256;
   const int64_t acc_elem = dtype == MLR_DTYPE_F64 ? 8 : 4;
@@ -354,10 +359,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                        (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 &&
                        q_stride_b % 8 == 0 && q_stride_h % 8 == 0;
   // The matrix-core kernel keeps token positions in 32 bits.
-  // The matrix-core kernel keeps one arrival counter per (sequence, KV head)
-  // in the workspace's fixed counter region.
   const bool mfma =
-      aligned && max_context < (int64_t(1) << 31) && batch * num_kv_heads <= kCounterSlots &&
+      aligned && max_context < (int64_t(1) << 31) &&
       decode_mfma_eligible(dtype, head_dim, num_q_heads / num_kv_heads, block_size);
   int64_t ts = tokens_per_split > 0 ? tokens_per_split
                                     : default_tokens_per_split(mfma, head_dim, max_context);
@@ -406,7 +409,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
   p.scale = scale;
   p.ts = static_cast<int>(ts);
   p.max_splits = static_cast<int>(max_splits);
-  p.ws_ctr = static_cast<int *>(workspace);
+  p.split_stride = static_cast<int>(ceil_div(max_splits, kSplitRowPad) * kSplitRowPad);
+  p.ws_flag = static_cast<uint32_t *>(workspace);
   p.ws_ml = reinterpret_cast<float2 *>(static_cast<unsigned char *>(workspace) + wl.ml_offset);
   p.ws_acc = static_cast<unsigned char *>(workspace) + wl.acc_offset;
   p.ml_base2 = mfma ? 1 : 0;
@@ -496,11 +500,11 @@ extern "C" int mlr_paged_decode_append(
 // ---------------------------------------------------------------------------
 namespace {
 
-// Decode scratch of the library on every GPU it runs on: the counter region
-// and the split partials of one call (8 MiB covers, for instance, 64
-// sequences x 28 query heads x 16 splits at head_dim 128). Each device holds
-// its own copy until the process ends. Static device memory starts zeroed, as
-// the counter region must; every call leaves the counters zero again.
+// Decode scratch of the library on every GPU it runs on: the flag region and
+// the split partials of one call (8 MiB covers, for instance, 64 sequences x
+// 14 query heads x 16 splits at head_dim 64). Each device holds its own copy
+// until the process ends. Static device memory starts zeroed, as a decode
+// workspace must; every call leaves it zero again.
 constexpr size_t kStaticScratchBytes = size_t(8) << 20;
 __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 

@@ -30,14 +30,19 @@
 // current one (two register buffers), so 8-16 KiB per wave are in flight.
 //
 // The four waves merge through LDS. A sequence that fits one split writes its
-// output directly; otherwise each workgroup stores its split's (m, l, acc)
-// with device-coherent stores and bumps the (sequence, KV head) counter, and
-// the workgroup that arrives last merges every split of the group:
-//   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s.
-// That saves the second launch of a separate combine kernel (about 1.9 us of
-// launch gap plus a memory round trip per step); the counters and partials
-// go through memory, not an XCD's L2, so the merge holds wherever the
-// hardware places the workgroups.
+// output directly; otherwise every split but the last stores its (m, l, acc)
+// to the workspace with device-coherent stores, each word encoded so that
+// zero means "not stored yet", and the workgroup of the last split (the
+// group's highest index, dispatched after the others) reads the rows until
+// every word has arrived and merges them with its own split:
+//   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s,
+// returning the rows to zero for the next call. That saves the second launch
+// of a separate combine kernel (about 1.9 us of launch gap plus a memory
+// round trip per step), and, against a merge by the last split to finish
+// (stores, wait for them, bump a counter, read), two of the three dependent
+// memory round trips at the end of the step. The partials go through memory,
+// not an XCD's L2, so the merge holds wherever the hardware places the
+// workgroups.
 //
 // Scores are rounded like the reference's bf16 matmul (to bf16, times scale,
 // to bf16 again: kernels/reference/paged_attention.py:246-247) before the
@@ -391,16 +396,23 @@ __device__ __forceinline__ WorkItem find_item(const DecodeParams &p, int j, int6
 // policy, bit 4 of the buffer intrinsics' aux operand on gfx950): stores are
 // written through to memory and loads are not served from a possibly stale
 // L2 line, so a workgroup on any XCD reads what another wrote once the
-// writer's stores completed and the group counter moved. Plain buffer loads,
-// not atomic ones: relaxed atomic loads whose addresses might alias are
-// issued one at a time, these are issued back to back.
+// store has reached memory, and a read issued earlier returns the old word.
+// Plain buffer loads, not atomic ones: relaxed atomic loads whose addresses
+// might alias are issued one at a time, these are issued back to back.
 constexpr int kCoherent = 16;
-__device__ __forceinline__ void store_shared(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kCoherent);
+
+// A partial word in the workspace is the value's bits with the sign bit
+// flipped, after NaNs become the canonical quiet NaN and -0 becomes +0: no
+// value is stored as zero, so a word is zero exactly when its producer has
+// not stored it yet, and a zero word reads back as -0 (a finite value that a
+// zero weight cancels). Aligned 32-bit stores and loads are single-copy
+// atomic, so a word is read whole or not at all.
+__device__ __forceinline__ void publish(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  uint32_t u = v != v ? 0x7FC00000u : __float_as_uint(v);
+  u = u == 0x80000000u ? 0u : u;
+  __builtin_amdgcn_raw_buffer_store_b32(u ^ 0x80000000u, r, off, 0, kCoherent);
 }
-__device__ __forceinline__ float load_shared(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCoherent));
-}
+__device__ __forceinline__ float unpublish(uint32_t w) { return __uint_as_float(w ^ 0x80000000u); }
 
 // One work item (a split of one sequence, one KV head) for the workgroup.
 template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds>
@@ -623,73 +635,79 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   }
   __syncthreads();
 
-  // Merge the four waves. A sequence that fits one split is finished here;
-  // otherwise the split's (m, l, acc) go to the workspace (m as a base-2
-  // exponent) and the last split of the (sequence, KV head) to finish merges
-  // them all.
+  // Merge the four waves. A sequence that fits one split is finished here.
+  // Otherwise splits 0 .. nsplits - 2 publish their (m, l, acc) rows to the
+  // workspace (m as a base-2 exponent) and the group's last split merges
+  // them with its own, which it keeps: thread t holds the outputs
+  // t + 256 r of the group (head (t + 256 r) / D, dim (t + 256 r) % D).
   const int head0 = kvh * p.group;
   uint16_t *out = static_cast<uint16_t *>(p.out);
   // This group's partial rows: (m, l) pairs and acc rows for its heads h and
-  // splits s at row h * max_splits + s, under buffer resources of the group's
+  // splits s at row h * split_stride + s, under buffer resources of the group's
   // span (at most 16 heads x 8192 splits x 128 dims of FP32: 32-bit offsets).
   const int64_t row_b = (int64_t)b * p.hq + head0;
-  const int rows_g = p.group * p.max_splits;
+  const int rows_g = p.group * p.split_stride;
   const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(
-      static_cast<float *>(p.ws_acc) + row_b * p.max_splits * D, 0,
+      static_cast<float *>(p.ws_acc) + row_b * p.split_stride * D, 0,
       static_cast<uint32_t>(rows_g) * D * 4u, 0x00020000);
   const __amdgpu_buffer_rsrc_t ml_r = __builtin_amdgcn_make_buffer_rsrc(
-      reinterpret_cast<float *>(p.ws_ml) + row_b * p.max_splits * 2, 0,
+      reinterpret_cast<float *>(p.ws_ml) + row_b * p.split_stride * 2, 0,
       static_cast<uint32_t>(rows_g) * 8u, 0x00020000);
-  for (int idx = threadIdx.x; idx < p.group * D; idx += blockDim.x) {
-    const int h = idx / D, d = idx % D;
-    float M = m_s[0][h];
+  const bool merger = nsplits > 1 && split == nsplits - 1;
+  constexpr int kMaxOut = (16 * D + 255) / 256;  // outputs per thread, at most
+  const int nout = p.group * D;
+  float own[kMaxOut];
+  __shared__ float own_m_s[16], own_l_s[16];
 #pragma unroll
-    for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, m_s[ww][h]);
-    float num = 0.f, den = 0.f;
+  for (int r = 0; r < kMaxOut; ++r) {
+    const int idx = threadIdx.x + 256 * r;
+    own[r] = 0.f;
+    if (idx < nout) {
+      const int h = idx / D, d = idx % D;
+      float M = m_s[0][h];
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
-      const float f = __builtin_amdgcn_exp2f(m_s[ww][h] - M);
-      num += f * o_s[ww][h][d];
-      den += f * l_s[ww][h];
-    }
-    if (nsplits == 1) {
-      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num / den);
-    } else {
-      const uint32_t row = static_cast<uint32_t>(h * p.max_splits + split);
-      store_shared(acc_r, (row * D + d) * 4u, num);
-      if (d == 0) {
-        store_shared(ml_r, row * 8u, M);
-        store_shared(ml_r, row * 8u + 4u, den);
+      for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, m_s[ww][h]);
+      float num = 0.f, den = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const float f = __builtin_amdgcn_exp2f(m_s[ww][h] - M);
+        num += f * o_s[ww][h][d];
+        den += f * l_s[ww][h];
+      }
+      if (nsplits == 1) {
+        out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num / den);
+      } else if (merger) {
+        own[r] = num;
+        if (d == 0) {
+          own_m_s[h] = M;
+          own_l_s[h] = den;
+        }
+      } else {
+        const uint32_t row = static_cast<uint32_t>(h * p.split_stride + split);
+        publish(acc_r, (row * D + d) * 4u, num);
+        if (d == 0) {
+          publish(ml_r, row * 8u, M);
+          publish(ml_r, row * 8u + 4u, den);
+        }
       }
     }
   }
-  if (nsplits == 1) return;
+  if (!merger) return;
 
-  // Arrival: every thread's partial stores have completed before the group
-  // counter moves. On gfx9 stores count in vmcnt, so waiting for vmcnt(0)
-  // waits for their acknowledgement at device scope (the stores are
-  // write-through); a workgroup-scope fence would not wait for them. The
-  // workgroup that brings the counter to nsplits - 1 is the last and returns
-  // it to zero for the next call (it is the counter's last user in this one).
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  __shared__ int last_s;
-  if (threadIdx.x == 0) {
-    int *ctr = p.ws_ctr + b * p.hkv + kvh;
-    const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_s = old == nsplits - 1;
-    if (old == nsplits - 1)
-      __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last_s) return;
-
-  // The group merge, in split order whatever the arrival order (the result
-  // does not depend on which split finished last):
-  //   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s,
-  // kChunk splits per memory round trip, chunks after the first rescaling
-  // the running sums.
+  // The group merge, in split order: splits 0 .. nsplits - 2 from the
+  // workspace, kChunk per round trip, then this workgroup's own split:
+  //   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s.
+  // A chunk is read again until every word of it has arrived (none is zero).
+  // Its producers are workgroups of lower index, dispatched before this one:
+  // they hold or held a slot and finish without waiting on anything, so the
+  // wait ends; a wait past kMaxPolls reads means that assumption failed, and
+  // the merge then records the failure in the workspace's flag word and
+  // writes NaN. Words that were read are returned to zero.
   constexpr int kChunk = 16;
+  constexpr int kMaxPolls = 1 << 17;
+  static_assert(kSplitRowPad % kChunk == 0, "a chunk's rows stay inside one head's rows");
+  __shared__ float mc_s[16][kChunk];   // the chunk's m per (head, split)
+  __shared__ float lc_s[16][kChunk];   // the chunk's l per (head, split)
   __shared__ float f_s[kChunk][16];    // 2^{m_s - M_new} of the chunk's splits
   __shared__ float rescale_s[16];      // 2^{M_old - M_new} per head
   __shared__ float den_s[16];
@@ -698,64 +716,117 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     den_s[threadIdx.x] = 0.f;
     mrun_s[threadIdx.x] = -INFINITY;
   }
-  constexpr int kMaxOut = (16 * D + 255) / 256;  // outputs per thread, at most
   // Outputs per thread whose partial rows are in flight together: two cover
   // every group of up to 512 outputs (group * head_dim) in one pass.
   constexpr int kPre = 2;
-  const int nout = p.group * D;
+  const int nprev = nsplits - 1;
+  // Thread t reads the (m, l) pair of head t / kChunk, split s0 + t % kChunk
+  // (threads past the group read head 0's: neither checked nor used).
+  const int mh = threadIdx.x / kChunk, ms = threadIdx.x % kChunk;
+  const bool ml_real = mh < p.group;
+  // A flag word left by an earlier merge that gave up: the workspace may hold
+  // stale rows, so nothing read from it can be trusted.
+  bool failed = __builtin_amdgcn_readfirstlane(
+                    __builtin_amdgcn_raw_buffer_load_b32(
+                        __builtin_amdgcn_make_buffer_rsrc(p.ws_flag, 0, 4u, 0x00020000), 0u, 0,
+                        kCoherent)) != 0u;
   float num[kMaxOut];
 #pragma unroll
   for (int r = 0; r < kMaxOut; ++r) num[r] = 0.f;
-  for (int s0 = 0; s0 < nsplits; s0 += kChunk) {
-    const int cnt = min(kChunk, nsplits - s0);
+  for (int s0 = 0; s0 < nprev && !failed; s0 += kChunk) {
+    const int cnt = min(kChunk, nprev - s0);
+    const uint32_t live = (1u << cnt) - 1u;  // the chunk's splits, as bits
+    const uint32_t mloff =
+        static_cast<uint32_t>((ml_real ? mh : 0) * p.split_stride + s0 + ms) * 8u;
 #pragma unroll
     for (int pass = 0; pass < kMaxOut / kPre; ++pass) {
       if (pass * kPre * 256 >= nout) break;  // uniform
-      // Partial rows of this pass's outputs; on the first pass they are
-      // issued before the chunk's weights are known. Every load is issued
-      // (outputs past the group read head 0's row, rows past cnt repeat the
-      // last one: in bounds, and their weight is zero or they are not used),
-      // so that all of them are in flight together.
-      float a[kPre][kChunk];
+      // Per thread one byte offset per output at split s0; split s0 + s is
+      // s * D * 4 bytes further (an immediate offset). All kChunk rows are
+      // read: they lie inside the head's rows (split_stride is a multiple of
+      // kChunk), and those past cnt are neither checked nor used (they hold
+      // zero, which reads as -0, and their weight is 0).
+      // (Signed offsets: their sums cannot wrap, so the constant part can go
+      // to the instruction's immediate offset field.)
+      int abase[kPre];
 #pragma unroll
       for (int r = 0; r < kPre; ++r) {
         const int idx = threadIdx.x + 256 * (pass * kPre + r);
         const int h = idx < nout ? idx / D : 0, d = idx % D;
+        abase[r] = ((h * p.split_stride + s0) * D + d) * 4;
+      }
+      uint32_t a[kPre][kChunk], mw = 0, lw = 0;
+      for (int tries = 0;; ++tries) {
+        // Opaque to the optimiser, so that the split offsets are added inside
+        // the loop and land in the loads' immediate fields instead of being
+        // hoisted into one register per load.
+#pragma unroll
+        for (int r = 0; r < kPre; ++r) asm volatile("" : "+v"(abase[r]));
 #pragma unroll
         for (int s = 0; s < kChunk; ++s) {
-          const uint32_t row = static_cast<uint32_t>(h * p.max_splits + s0 + min(s, cnt - 1));
-          a[r][s] = load_shared(acc_r, (row * D + d) * 4u);
+#pragma unroll
+          for (int r = 0; r < kPre; ++r)
+            a[r][s] = __builtin_amdgcn_raw_buffer_load_b32(acc_r, abase[r] + s * D * 4, 0,
+                                                           kCoherent);
+        }
+        if (pass == 0) {
+          mw = __builtin_amdgcn_raw_buffer_load_b32(ml_r, mloff, 0, kCoherent);
+          lw = __builtin_amdgcn_raw_buffer_load_b32(ml_r, mloff + 4u, 0, kCoherent);
+        }
+        // Zero words as a bit mask over the chunk's splits, then one test
+        // against the splits that exist.
+        bool missing = false;
+#pragma unroll
+        for (int r = 0; r < kPre; ++r) {
+          uint32_t z = 0;
+#pragma unroll
+          for (int s = 0; s < kChunk; ++s) z |= (a[r][s] == 0u ? 1u : 0u) << s;
+          missing |= threadIdx.x + 256 * (pass * kPre + r) < nout && (z & live) != 0u;
+        }
+        if (pass == 0) missing |= ml_real && ms < cnt && (mw == 0u || lw == 0u);
+        if (!__syncthreads_or(missing)) break;  // uniform
+        if (tries == kMaxPolls) {
+          failed = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (failed) break;  // uniform
+      // Every word of the pass has arrived: return them to zero.
+#pragma unroll
+      for (int r = 0; r < kPre; ++r) asm volatile("" : "+v"(abase[r]));
+#pragma unroll
+      for (int s = 0; s < kChunk; ++s) {
+        if (s < cnt) {  // uniform
+#pragma unroll
+          for (int r = 0; r < kPre; ++r)
+            if (threadIdx.x + 256 * (pass * kPre + r) < nout)
+              __builtin_amdgcn_raw_buffer_store_b32(0u, acc_r, abase[r] + s * D * 4, 0,
+                                                    kCoherent);
         }
       }
       if (pass == 0) {
-        // The chunk's (m, l) per head, loaded by every lane of wave 0 (lanes
-        // past the group read the last head's: no divergent branch around
-        // the loads), in the same round trip as the partial rows above.
-        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        float m[kChunk], l[kChunk];
-        if (w == 0) {
-          const int hl = min(static_cast<int>(threadIdx.x), p.group - 1);
-#pragma unroll
-          for (int s = 0; s < kChunk; ++s) {
-            const uint32_t row = static_cast<uint32_t>(hl * p.max_splits + s0 + min(s, cnt - 1));
-            m[s] = load_shared(ml_r, row * 8u);
-            l[s] = load_shared(ml_r, row * 8u + 4u);
-          }
+        if (ml_real && ms < cnt) {
+          __builtin_amdgcn_raw_buffer_store_b32(0u, ml_r, mloff, 0, kCoherent);
+          __builtin_amdgcn_raw_buffer_store_b32(0u, ml_r, mloff + 4u, 0, kCoherent);
         }
-        __syncthreads();  // the previous chunk's weights are consumed
+        if (mh < 16) {
+          mc_s[mh][ms] = ms < cnt ? unpublish(mw) : -INFINITY;
+          lc_s[mh][ms] = unpublish(lw);
+        }
+        __syncthreads();
         if (threadIdx.x < p.group) {
           const int h = threadIdx.x;
           float m_new = mrun_s[h];
 #pragma unroll
-          for (int s = 0; s < kChunk; ++s)
-            if (s < cnt) m_new = fmaxf(m_new, m[s]);
+          for (int s = 0; s < kChunk; ++s) m_new = fmaxf(m_new, mc_s[h][s]);
           const float rs = __builtin_amdgcn_exp2f(mrun_s[h] - m_new);  // 0 on the first chunk
           float den = den_s[h] * rs;
 #pragma unroll
           for (int s = 0; s < kChunk; ++s) {
-            const float f = s < cnt ? __builtin_amdgcn_exp2f(m[s] - m_new) : 0.f;
+            const float f = s < cnt ? __builtin_amdgcn_exp2f(mc_s[h][s] - m_new) : 0.f;
             f_s[s][h] = f;
-            den += f * l[s];
+            den += f * lc_s[h][s];
           }
           rescale_s[h] = rs;
           den_s[h] = den;
@@ -770,19 +841,44 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
           const int h = idx / D;
           float acc = num[pass * kPre + r] * rescale_s[h];
 #pragma unroll
-          for (int s = 0; s < kChunk; ++s) acc += f_s[s][h] * a[r][s];  // f = 0 past cnt
+          for (int s = 0; s < kChunk; ++s)
+            acc += f_s[s][h] * unpublish(a[r][s]);  // rows past cnt: f = 0, word 0 (-0)
           num[pass * kPre + r] = acc;
         }
       }
     }
   }
+  if (failed) {
+    if (threadIdx.x == 0)
+      __builtin_amdgcn_raw_buffer_store_b32(
+          1u, __builtin_amdgcn_make_buffer_rsrc(p.ws_flag, 0, 4u, 0x00020000), 0u, 0, kCoherent);
+#pragma unroll
+    for (int r = 0; r < kMaxOut; ++r) {
+      const int idx = threadIdx.x + 256 * r;
+      if (idx < nout)
+        out[b * p.o_sb + (int64_t)(head0 + idx / D) * p.o_sh + idx % D] = 0x7FC0u;  // bf16 NaN
+    }
+    return;
+  }
+  // This workgroup's own split, last in split order.
+  __syncthreads();  // the last chunk's weights are consumed
+  if (threadIdx.x < p.group) {
+    const int h = threadIdx.x;
+    const float m_new = fmaxf(mrun_s[h], own_m_s[h]);
+    const float rs = __builtin_amdgcn_exp2f(mrun_s[h] - m_new);
+    const float f = __builtin_amdgcn_exp2f(own_m_s[h] - m_new);
+    den_s[h] = den_s[h] * rs + f * own_l_s[h];
+    rescale_s[h] = rs;
+    f_s[0][h] = f;
+  }
+  __syncthreads();
 #pragma unroll
   for (int r = 0; r < kMaxOut; ++r) {
     const int idx = threadIdx.x + 256 * r;
-    if (idx < p.group * D) {
+    if (idx < nout) {
       const int h = idx / D, d = idx % D;
-      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] =
-          float_to_bf16_bits(num[r] / den_s[h]);
+      const float v = (num[r] * rescale_s[h] + f_s[0][h] * own[r]) / den_s[h];
+      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(v);
     }
   }
 }

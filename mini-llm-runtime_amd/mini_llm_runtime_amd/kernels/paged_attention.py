@@ -54,10 +54,10 @@ def _require_kernel_layout(q: torch.Tensor, k_cache: torch.Tensor,
 
 
 # Decode workspaces by (device, stream): zero-filled when allocated. The
-# matrix-core decode keeps per-(sequence, KV head) arrival counters at the
-# front of the workspace; they must be zero when a call starts, and every call
-# leaves them zero. One workspace per stream keeps calls on different streams
-# from sharing counters or partials.
+# decode kernels exchange split partials through the workspace, a zero word
+# meaning "not written yet"; it must be zero when a call starts, and every
+# call leaves it zero. One workspace per stream keeps calls on different
+# streams from sharing partials.
 _WORKSPACES: dict = {}
 
 

@@ -49,19 +49,23 @@ def test_loader_binds_prototypes():
 
 def test_workspace_size_is_host_arithmetic():
     lib = _lib.load()
-    # D=64, 4096 tokens: 256-token splits. A fixed region of 65536 int counters,
-    # then 64 x 14 heads x 16 splits of (m, l), then acc; each part 256-aligned.
+    # D=64, 4096 tokens: 256-token splits. A 256-byte flag region, then
+    # 64 x 14 heads x 16 split rows of (m, l), then acc; each part
+    # 256-aligned, split rows per head a multiple of 16.
     size = lib.mlr_paged_decode_workspace_size(64, 14, 64, 4096, 0, 2)
     rows = 64 * 14 * 16
-    counters = 65536 * 4
+    flags = 256
     ml = (rows * 8 + 255) // 256 * 256
-    assert size == counters + ml + rows * 64 * 4
+    assert size == flags + ml + rows * 64 * 4
     # Short contexts: the generic kernel's default split is an eighth of the
-    # context (32 tokens here, 8 splits), the smallest default, so the size
-    # covers it whichever kernel the call takes.
+    # context (32 tokens here, 8 splits, padded to 16 rows), the smallest
+    # default, so the size covers it whichever kernel the call takes.
     size = lib.mlr_paged_decode_workspace_size(4, 14, 64, 256, 0, 0)
-    rows = 4 * 14 * 8
-    assert size == counters + (rows * 8 + 255) // 256 * 256 + rows * 64 * 4
+    rows = 4 * 14 * 16
+    assert size == flags + (rows * 8 + 255) // 256 * 256 + rows * 64 * 4
+    # 13 splits (320-token splits over 4096 tokens) also take 16 rows.
+    assert (lib.mlr_paged_decode_workspace_size(64, 14, 64, 4096, 320, 2)
+            == lib.mlr_paged_decode_workspace_size(64, 14, 64, 4096, 256, 2))
     assert lib.mlr_paged_decode_workspace_size(0, 14, 64, 4096, 0, 2) == 0
 
 
