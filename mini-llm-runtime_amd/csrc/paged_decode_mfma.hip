@@ -350,32 +350,44 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
   return x;
 }
 
-// Where one work item lies: sequence b, split, the sequence's clamped
-// context length and split count, and the number of items of the launch.
+// Where one work item lies: sequence b, split, and the sequence's clamped
+// context length and split count.
 struct WorkItem {
-  int b;      // -1: past the last live item
+  int b;  // -1: past the last live item
   int split;
   int ctx;
   int ns;
-  int total;  // live (sequence, split) items over the whole batch
 };
 
-// Work items are the live (sequence, split) pairs, sequence-major: item j is
-// split j - first(b) of the sequence b whose items cover j, where sequence b
-// has ns_b = ceil(ctx_b / ts) items. Every wave derives the same answer from
-// the context lengths (64 per round trip), so no workgroup is spent on a
-// split past its sequence's end, and no host-side prefix is needed.
+// Work items are the live (sequence, split) pairs, sequence b having
+// ns_b = ceil(ctx_b / ts) splits, in three runs:
+//   1. every split but the last of each sequence with two or more splits,
+//      sequence by sequence in split order (the producers of the merge);
+//   2. the last splits of those sequences, which merge their sequence's
+//      splits: dispatched after every split they wait for, and, with their
+//      own tokens streamed after the producers', they usually find the
+//      partials already published;
+//   3. the sequences that fit one split (nothing to merge).
+// Every wave derives the same answer from the context lengths (64 per round
+// trip), so no workgroup is spent on a split past its sequence's end, and no
+// host-side prefix is needed.
 __device__ __forceinline__ WorkItem find_item(const DecodeParams &p, int j, int64_t cap) {
   const int lane = threadIdx.x & 63;
-  WorkItem it{-1, 0, 0, 0, 0};
-  int carry = 0;
-  for (int c0 = 0; c0 < p.batch; c0 += 64) {
+  WorkItem it{-1, 0, 0, 0};
+  auto splits_of = [&](int c0, int &ctx) -> int {
     const int idx = c0 + lane;
-    int64_t c = idx < p.batch ? p.ctx[idx] : 0;
+    int64_t c = idx < p.batch ? p.ctx[idx] : 0;  // lanes past the batch: no splits
     c = c < 0 ? 0 : (c > cap ? cap : c);
-    const int ctx = static_cast<int>(c);  // < 2^31 on this path
-    const int ns = (ctx + p.ts - 1) / p.ts;
-    const int incl = carry + wave_inclusive_scan(ns);
+    ctx = static_cast<int>(c);  // < 2^31 on this path
+    return (ctx + p.ts - 1) / p.ts;
+  };
+  // Run 1, and the number of sequences with two or more splits.
+  int carry = 0, nmerge = 0;
+  for (int c0 = 0; c0 < p.batch; c0 += 64) {
+    int ctx;
+    const int ns = splits_of(c0, ctx);
+    const int np = ns > 1 ? ns - 1 : 0;
+    const int incl = carry + wave_inclusive_scan(np);
     const int total = __builtin_amdgcn_readlane(incl, 63);
     if (it.b < 0 && j >= carry && j < total) {  // uniform: the item lies in this chunk
       // Sequences wholly before item j are the lanes whose prefix is <= j
@@ -383,12 +395,36 @@ __device__ __forceinline__ WorkItem find_item(const DecodeParams &p, int j, int6
       const int bl = __popcll(__ballot(incl <= j));
       it.b = c0 + bl;
       it.ns = __builtin_amdgcn_readlane(ns, bl);
-      it.split = j - (__builtin_amdgcn_readlane(incl, bl) - it.ns);
+      it.split = j - (__builtin_amdgcn_readlane(incl, bl) - __builtin_amdgcn_readlane(np, bl));
       it.ctx = __builtin_amdgcn_readlane(ctx, bl);
     }
     carry = total;
+    nmerge += __popcll(__ballot(ns > 1));
   }
-  it.total = carry;
+  if (it.b >= 0) return it;
+  // Runs 2 and 3: the k-th sequence with two or more splits (its last
+  // split), else the k-th sequence with one split.
+  int k = j - carry;
+  const bool merging = k < nmerge;
+  if (!merging) k -= nmerge;
+  int before = 0;
+  for (int c0 = 0; c0 < p.batch; c0 += 64) {
+    int ctx;
+    const int ns = splits_of(c0, ctx);
+    const uint64_t sel = __ballot(merging ? ns > 1 : ns == 1);
+    const int cnt = __popcll(sel);
+    if (k < before + cnt) {  // uniform
+      // The selected lane with k - before selected lanes below it.
+      const int upto = __popcll(sel & ((2ull << lane) - 1));  // selected lanes <= this one
+      const int bl = __popcll(__ballot(upto <= k - before));
+      it.b = c0 + bl;
+      it.ns = __builtin_amdgcn_readlane(ns, bl);
+      it.split = merging ? it.ns - 1 : 0;
+      it.ctx = __builtin_amdgcn_readlane(ctx, bl);
+      break;
+    }
+    before += cnt;
+  }
   return it;
 }
 
@@ -695,20 +731,22 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   if (!merger) return;
 
   // The group merge, in split order: splits 0 .. nsplits - 2 from the
-  // workspace, kChunk per round trip, then this workgroup's own split:
+  // workspace, kChunk per round trip, and this workgroup's own split folded
+  // in with the last chunk:
   //   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s.
   // A chunk is read again until every word of it has arrived (none is zero).
   // Its producers are workgroups of lower index, dispatched before this one:
   // they hold or held a slot and finish without waiting on anything, so the
   // wait ends; a wait past kMaxPolls reads means that assumption failed, and
   // the merge then records the failure in the workspace's flag word and
-  // writes NaN. Words that were read are returned to zero.
+  // writes NaN (as it does when the flag word was already set). Words that
+  // were read are returned to zero.
   constexpr int kChunk = 16;
   constexpr int kMaxPolls = 1 << 17;
   static_assert(kSplitRowPad % kChunk == 0, "a chunk's rows stay inside one head's rows");
   __shared__ float mc_s[16][kChunk];   // the chunk's m per (head, split)
   __shared__ float lc_s[16][kChunk];   // the chunk's l per (head, split)
-  __shared__ float f_s[kChunk][16];    // 2^{m_s - M_new} of the chunk's splits
+  __shared__ float f_s[kChunk + 1][16];  // 2^{m_s - M_new}: the chunk's splits, then own
   __shared__ float rescale_s[16];      // 2^{M_old - M_new} per head
   __shared__ float den_s[16];
   __shared__ float mrun_s[16];
@@ -724,17 +762,19 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // (threads past the group read head 0's: neither checked nor used).
   const int mh = threadIdx.x / kChunk, ms = threadIdx.x % kChunk;
   const bool ml_real = mh < p.group;
-  // A flag word left by an earlier merge that gave up: the workspace may hold
-  // stale rows, so nothing read from it can be trusted.
-  bool failed = __builtin_amdgcn_readfirstlane(
-                    __builtin_amdgcn_raw_buffer_load_b32(
-                        __builtin_amdgcn_make_buffer_rsrc(p.ws_flag, 0, 4u, 0x00020000), 0u, 0,
-                        kCoherent)) != 0u;
+  // The workspace's flag word: set by an earlier merge that gave up, it
+  // means the workspace may hold stale rows, so nothing read from it can be
+  // trusted. Read with the first chunk, in the same round trip.
+  const __amdgpu_buffer_rsrc_t flag_r =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_flag, 0, 4u, 0x00020000);
+  __shared__ uint32_t flag_s;
+  bool failed = false;
   float num[kMaxOut];
 #pragma unroll
   for (int r = 0; r < kMaxOut; ++r) num[r] = 0.f;
   for (int s0 = 0; s0 < nprev && !failed; s0 += kChunk) {
     const int cnt = min(kChunk, nprev - s0);
+    const bool last = s0 + kChunk >= nprev;  // own split folds in here
     const uint32_t live = (1u << cnt) - 1u;  // the chunk's splits, as bits
     const uint32_t mloff =
         static_cast<uint32_t>((ml_real ? mh : 0) * p.split_stride + s0 + ms) * 8u;
@@ -784,7 +824,15 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
           missing |= threadIdx.x + 256 * (pass * kPre + r) < nout && (z & live) != 0u;
         }
         if (pass == 0) missing |= ml_real && ms < cnt && (mw == 0u || lw == 0u);
-        if (!__syncthreads_or(missing)) break;  // uniform
+        const bool first = s0 == 0 && pass == 0 && tries == 0;  // uniform
+        if (first && threadIdx.x == 0)
+          flag_s = __builtin_amdgcn_raw_buffer_load_b32(flag_r, 0u, 0, kCoherent);
+        const bool any_missing = __syncthreads_or(missing);  // uniform
+        if (first && flag_s != 0u) {  // uniform: read by all after the barrier
+          failed = true;
+          break;
+        }
+        if (!any_missing) break;
         if (tries == kMaxPolls) {
           failed = true;
           break;
@@ -792,7 +840,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         __builtin_amdgcn_s_sleep(2);
       }
       if (failed) break;  // uniform
-      // Every word of the pass has arrived: return them to zero.
+      // Every word of the pass has arrived: return them to zero. (Threads
+      // past the group's outputs point at head 0's words of the chunk, which
+      // were read too: storing zero there again needs no per-lane test.)
 #pragma unroll
       for (int r = 0; r < kPre; ++r) asm volatile("" : "+v"(abase[r]));
 #pragma unroll
@@ -800,9 +850,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         if (s < cnt) {  // uniform
 #pragma unroll
           for (int r = 0; r < kPre; ++r)
-            if (threadIdx.x + 256 * (pass * kPre + r) < nout)
-              __builtin_amdgcn_raw_buffer_store_b32(0u, acc_r, abase[r] + s * D * 4, 0,
-                                                    kCoherent);
+            __builtin_amdgcn_raw_buffer_store_b32(0u, acc_r, abase[r] + s * D * 4, 0, kCoherent);
         }
       }
       if (pass == 0) {
@@ -820,6 +868,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
           float m_new = mrun_s[h];
 #pragma unroll
           for (int s = 0; s < kChunk; ++s) m_new = fmaxf(m_new, mc_s[h][s]);
+          if (last) m_new = fmaxf(m_new, own_m_s[h]);
           const float rs = __builtin_amdgcn_exp2f(mrun_s[h] - m_new);  // 0 on the first chunk
           float den = den_s[h] * rs;
 #pragma unroll
@@ -828,6 +877,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
             f_s[s][h] = f;
             den += f * lc_s[h][s];
           }
+          const float f_own = last ? __builtin_amdgcn_exp2f(own_m_s[h] - m_new) : 0.f;
+          f_s[kChunk][h] = f_own;
+          den += f_own * own_l_s[h];
           rescale_s[h] = rs;
           den_s[h] = den;
           mrun_s[h] = m_new;
@@ -843,15 +895,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 #pragma unroll
           for (int s = 0; s < kChunk; ++s)
             acc += f_s[s][h] * unpublish(a[r][s]);  // rows past cnt: f = 0, word 0 (-0)
+          acc += f_s[kChunk][h] * own[pass * kPre + r];  // 0 before the last chunk
           num[pass * kPre + r] = acc;
         }
       }
     }
   }
   if (failed) {
-    if (threadIdx.x == 0)
-      __builtin_amdgcn_raw_buffer_store_b32(
-          1u, __builtin_amdgcn_make_buffer_rsrc(p.ws_flag, 0, 4u, 0x00020000), 0u, 0, kCoherent);
+    if (threadIdx.x == 0) __builtin_amdgcn_raw_buffer_store_b32(1u, flag_r, 0u, 0, kCoherent);
 #pragma unroll
     for (int r = 0; r < kMaxOut; ++r) {
       const int idx = threadIdx.x + 256 * r;
@@ -860,25 +911,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     }
     return;
   }
-  // This workgroup's own split, last in split order.
-  __syncthreads();  // the last chunk's weights are consumed
-  if (threadIdx.x < p.group) {
-    const int h = threadIdx.x;
-    const float m_new = fmaxf(mrun_s[h], own_m_s[h]);
-    const float rs = __builtin_amdgcn_exp2f(mrun_s[h] - m_new);
-    const float f = __builtin_amdgcn_exp2f(own_m_s[h] - m_new);
-    den_s[h] = den_s[h] * rs + f * own_l_s[h];
-    rescale_s[h] = rs;
-    f_s[0][h] = f;
-  }
-  __syncthreads();
 #pragma unroll
   for (int r = 0; r < kMaxOut; ++r) {
     const int idx = threadIdx.x + 256 * r;
     if (idx < nout) {
       const int h = idx / D, d = idx % D;
-      const float v = (num[r] * rescale_s[h] + f_s[0][h] * own[r]) / den_s[h];
-      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(v);
+      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num[r] / den_s[h]);
     }
   }
 }
