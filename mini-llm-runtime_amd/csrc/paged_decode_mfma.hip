@@ -1,12 +1,13 @@
 // bf16 split-KV paged decode on gfx950 matrix cores, in one launch.
 //
-// One workgroup of four wavefronts per (live split, KV head). A split is
+// One workgroup of four wavefronts per (live split, KV head), or of eight per
+// (live split, pair of KV heads), four for each head. A split is
 // tokens_per_split tokens of one sequence; the live splits of all sequences
 // are numbered sequence by sequence and every workgroup finds its own from a
 // prefix sum of the context lengths, so no workgroup is spent on a split past
 // a sequence's end (only the grid's tail, sized for the widest table, exits
 // at once). The split's
-// 16-token tiles are dealt round-robin to the four waves; each wave keeps the
+// 16-token tiles are dealt round-robin to a head's four waves; each wave keeps the
 // online-softmax state of all (<= 16) query heads of the KV head's GQA group,
 // so every K/V byte is read from HBM exactly once for the whole group.
 //
@@ -451,15 +452,23 @@ __device__ __forceinline__ void publish(__amdgpu_buffer_rsrc_t r, uint32_t off, 
 __device__ __forceinline__ float unpublish(uint32_t w) { return __uint_as_float(w ^ 0x80000000u); }
 
 // One work item (a split of one sequence, one KV head) for the workgroup.
-template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds>
+// kH KV heads per workgroup (1 or 2), kWaves waves each: waves
+// hs * kWaves .. + kWaves - 1 serve KV head kvh_base + hs over the same
+// tiles, so with kH = 2 both halves of every slot row are requested by one
+// workgroup at the same time.
+template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH>
 __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkItem &it,
-                                            int kvh) {
+                                            int kvh_base) {
   constexpr int QK = D / 32;
   constexpr int VC = D / 16;
+  constexpr int kThreads = 64 * kWaves * kH;
   const int lane = threadIdx.x & 63;
   // The wave index is uniform within a wave; saying so keeps every value
   // derived from it (tile counts, block ids, descriptors) in SGPRs.
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = wave % kWaves;   // the wave's place among its KV head's waves
+  const int hs = wave / kWaves;  // which of the workgroup's KV heads it serves
+  const int kvh = kvh_base + hs;
   const int m16 = lane & 15, g = lane >> 4;
   const int b = it.b, split = it.split, nsplits = it.ns;
   const int64_t ctx = it.ctx;
@@ -498,7 +507,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // Fused KV write: the new token's slot and its K/V rows (wave 0, 16 bytes
   // per lane) come with the prologue, so that staging them (LDS and cache,
   // by the workgroup that holds the token) waits for no tile load.
-  __shared__ __align__(16) uint16_t new_row_s[2 * D];
+  __shared__ __align__(16) uint16_t new_row_s[kH][2 * D];
   const int64_t new_slot = kAppend ? p.new_slots[b] : -1;
   const bool new_is_v = lane >= D / 8;
   const int new_off = 8 * (new_is_v ? lane - D / 8 : lane);
@@ -558,7 +567,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // them. Called once, after the first batch of tile loads is issued.
   auto stage_new_row = [&]() {
     if (w == 0 && lane < D / 4) {
-      *reinterpret_cast<uint4 *>(new_row_s + (new_is_v ? D : 0) + new_off) = new_chunk;
+      *reinterpret_cast<uint4 *>(new_row_s[hs] + (new_is_v ? D : 0) + new_off) = new_chunk;
       const int64_t num_slots = p.num_blocks * p.block_size;
       if (new_slot >= 0 && new_slot < num_slots) {
         uint16_t *dst = static_cast<uint16_t *>(new_is_v ? p.vc_w : p.kc_w) +
@@ -600,7 +609,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   auto compute = [&](Tile<D>(&buf)[kBatch]) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
-      compute_tile<D, kAppend>(st, buf[u], qf, scale, live, g, m16, new_row_s);
+      compute_tile<D, kAppend>(st, buf[u], qf, scale, live, g, m16, new_row_s[hs]);
   };
 
   // The workgroup holding the new token stages its rows once, after every
@@ -626,20 +635,20 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     // workgroup keeps 80 KB in flight and the splits of a batch like 64
     // sequences of up to 4K tokens fit the GPU in one generation.
     static_assert(D == 64 && kBatch == 4, "LDS landing is laid out for head_dim 64");
-    __shared__ __align__(16) unsigned char lds_tiles[kWaves][kLdsTileBytes];
+    __shared__ __align__(16) unsigned char lds_tiles[kWaves * kH][kLdsTileBytes];
     Tile<D> buf[kBatch];
     issue(buf, 0);
     const int rel4 = 16 * (w + kWaves * kBatch);
     const int blk4 = kBatch < nk ? __builtin_amdgcn_readlane(blk_reg, kBatch) : -1;
-    copy_tile_to_lds(lds_tiles[w], kc, vc, block_elems,
+    copy_tile_to_lds(lds_tiles[wave], kc, vc, block_elems,
                      static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel4)) * row_elems * 2,
                      blk4, kvh, row_elems * 2, lane);
     if (append_here) stage_new_row();
     compute(buf);
     if (kBatch < nk) {  // uniform
-      read_tile_from_lds(buf[0], lds_tiles[w], blk4, rel4, m16, g);
+      read_tile_from_lds(buf[0], lds_tiles[wave], blk4, rel4, m16, g);
       if (append_here && rel4 == last_rel) mark_new_row(buf[0]);
-      compute_tile<D, kAppend>(st, buf[0], qf, scale, live, g, m16, new_row_s);
+      compute_tile<D, kAppend>(st, buf[0], qf, scale, live, g, m16, new_row_s[hs]);
     }
   } else {
     // Issued whatever nk is (absent tiles read zeros), so that every path
@@ -656,33 +665,36 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // Per-head l: sum the four lanes that share the head.
   st.l = sum_xor32(sum_xor16(st.l));
 
-  __shared__ float o_s[kWaves][16][D + 4];
-  __shared__ float m_s[kWaves][16];
-  __shared__ float l_s[kWaves][16];
+  __shared__ float o_s[kWaves * kH][16][D + 4];
+  __shared__ float m_s[kWaves * kH][16];
+  __shared__ float l_s[kWaves * kH][16];
   if (g == 0) {
-    m_s[w][m16] = st.m;
-    l_s[w][m16] = st.l;
+    m_s[wave][m16] = st.m;
+    l_s[wave][m16] = st.l;
   }
   // Lane l holds O[head l%16][dims VC*(4g+i) + n].
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int n = 0; n < VC; ++n) o_s[w][m16][VC * (4 * g + i) + n] = st.acc[n][i];
+    for (int n = 0; n < VC; ++n) o_s[wave][m16][VC * (4 * g + i) + n] = st.acc[n][i];
   }
   __syncthreads();
 
-  // Merge the four waves. A sequence that fits one split is finished here.
-  // Otherwise splits 0 .. nsplits - 2 publish their (m, l, acc) rows to the
-  // workspace (m as a base-2 exponent) and the group's last split merges
-  // them with its own, which it keeps: thread t holds the outputs
-  // t + 256 r of the group (head (t + 256 r) / D, dim (t + 256 r) % D).
-  const int head0 = kvh * p.group;
+  // Merge the waves of each KV head. A sequence that fits one split is
+  // finished here. Otherwise splits 0 .. nsplits - 2 publish their (m, l,
+  // acc) rows to the workspace (m as a base-2 exponent) and the sequence's
+  // last split merges them with its own, which it keeps. The workgroup's
+  // query heads are the kH GQA groups of its KV heads, ngh in all; thread t
+  // holds the outputs t + kThreads r (head (t + kThreads r) / D, dim
+  // (t + kThreads r) % D).
+  const int ngh = kH * p.group;
+  const int head0 = kvh_base * p.group;
   uint16_t *out = static_cast<uint16_t *>(p.out);
-  // This group's partial rows: (m, l) pairs and acc rows for its heads h and
-  // splits s at row h * split_stride + s, under buffer resources of the group's
+  // The workgroup's partial rows: (m, l) pairs and acc rows for its heads h
+  // and splits s at row h * split_stride + s, under buffer resources of their
   // span (at most 16 heads x 8192 splits x 128 dims of FP32: 32-bit offsets).
   const int64_t row_b = (int64_t)b * p.hq + head0;
-  const int rows_g = p.group * p.split_stride;
+  const int rows_g = ngh * p.split_stride;
   const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(
       static_cast<float *>(p.ws_acc) + row_b * p.split_stride * D, 0,
       static_cast<uint32_t>(rows_g) * D * 4u, 0x00020000);
@@ -690,25 +702,28 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       reinterpret_cast<float *>(p.ws_ml) + row_b * p.split_stride * 2, 0,
       static_cast<uint32_t>(rows_g) * 8u, 0x00020000);
   const bool merger = nsplits > 1 && split == nsplits - 1;
-  constexpr int kMaxOut = (16 * D + 255) / 256;  // outputs per thread, at most
-  const int nout = p.group * D;
+  constexpr int kMaxOut = (16 * D + kThreads - 1) / kThreads;  // outputs per thread, at most
+  const int nout = ngh * D;
   float own[kMaxOut];
   __shared__ float own_m_s[16], own_l_s[16];
 #pragma unroll
   for (int r = 0; r < kMaxOut; ++r) {
-    const int idx = threadIdx.x + 256 * r;
+    const int idx = threadIdx.x + kThreads * r;
     own[r] = 0.f;
     if (idx < nout) {
       const int h = idx / D, d = idx % D;
-      float M = m_s[0][h];
+      // Waves w0 .. w0 + kWaves - 1 hold head h (head hg of their group).
+      const int w0 = kH == 1 ? 0 : (h / p.group) * kWaves;
+      const int hg = kH == 1 ? h : h % p.group;
+      float M = m_s[w0][hg];
 #pragma unroll
-      for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, m_s[ww][h]);
+      for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, m_s[w0 + ww][hg]);
       float num = 0.f, den = 0.f;
 #pragma unroll
       for (int ww = 0; ww < kWaves; ++ww) {
-        const float f = __builtin_amdgcn_exp2f(m_s[ww][h] - M);
-        num += f * o_s[ww][h][d];
-        den += f * l_s[ww][h];
+        const float f = __builtin_amdgcn_exp2f(m_s[w0 + ww][hg] - M);
+        num += f * o_s[w0 + ww][hg][d];
+        den += f * l_s[w0 + ww][hg];
       }
       if (nsplits == 1) {
         out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num / den);
@@ -755,13 +770,13 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     mrun_s[threadIdx.x] = -INFINITY;
   }
   // Outputs per thread whose partial rows are in flight together: two cover
-  // every group of up to 512 outputs (group * head_dim) in one pass.
+  // up to 2 * kThreads outputs (ngh * head_dim) in one pass.
   constexpr int kPre = 2;
   const int nprev = nsplits - 1;
   // Thread t reads the (m, l) pair of head t / kChunk, split s0 + t % kChunk
   // (threads past the group read head 0's: neither checked nor used).
   const int mh = threadIdx.x / kChunk, ms = threadIdx.x % kChunk;
-  const bool ml_real = mh < p.group;
+  const bool ml_real = mh < ngh;
   // The workspace's flag word: set by an earlier merge that gave up, it
   // means the workspace may hold stale rows, so nothing read from it can be
   // trusted. Read with the first chunk, in the same round trip.
@@ -780,7 +795,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         static_cast<uint32_t>((ml_real ? mh : 0) * p.split_stride + s0 + ms) * 8u;
 #pragma unroll
     for (int pass = 0; pass < kMaxOut / kPre; ++pass) {
-      if (pass * kPre * 256 >= nout) break;  // uniform
+      if (pass * kPre * kThreads >= nout) break;  // uniform
       // Per thread one byte offset per output at split s0; split s0 + s is
       // s * D * 4 bytes further (an immediate offset). All kChunk rows are
       // read: they lie inside the head's rows (split_stride is a multiple of
@@ -791,7 +806,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       int abase[kPre];
 #pragma unroll
       for (int r = 0; r < kPre; ++r) {
-        const int idx = threadIdx.x + 256 * (pass * kPre + r);
+        const int idx = threadIdx.x + kThreads * (pass * kPre + r);
         const int h = idx < nout ? idx / D : 0, d = idx % D;
         abase[r] = ((h * p.split_stride + s0) * D + d) * 4;
       }
@@ -821,7 +836,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
           uint32_t z = 0;
 #pragma unroll
           for (int s = 0; s < kChunk; ++s) z |= (a[r][s] == 0u ? 1u : 0u) << s;
-          missing |= threadIdx.x + 256 * (pass * kPre + r) < nout && (z & live) != 0u;
+          missing |= threadIdx.x + kThreads * (pass * kPre + r) < nout && (z & live) != 0u;
         }
         if (pass == 0) missing |= ml_real && ms < cnt && (mw == 0u || lw == 0u);
         const bool first = s0 == 0 && pass == 0 && tries == 0;  // uniform
@@ -863,7 +878,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
           lc_s[mh][ms] = unpublish(lw);
         }
         __syncthreads();
-        if (threadIdx.x < p.group) {
+        if (threadIdx.x < ngh) {
           const int h = threadIdx.x;
           float m_new = mrun_s[h];
 #pragma unroll
@@ -888,7 +903,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       }
 #pragma unroll
       for (int r = 0; r < kPre; ++r) {
-        const int idx = threadIdx.x + 256 * (pass * kPre + r);
+        const int idx = threadIdx.x + kThreads * (pass * kPre + r);
         if (idx < nout) {
           const int h = idx / D;
           float acc = num[pass * kPre + r] * rescale_s[h];
@@ -905,7 +920,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     if (threadIdx.x == 0) __builtin_amdgcn_raw_buffer_store_b32(1u, flag_r, 0u, 0, kCoherent);
 #pragma unroll
     for (int r = 0; r < kMaxOut; ++r) {
-      const int idx = threadIdx.x + 256 * r;
+      const int idx = threadIdx.x + kThreads * r;
       if (idx < nout)
         out[b * p.o_sb + (int64_t)(head0 + idx / D) * p.o_sh + idx % D] = 0x7FC0u;  // bf16 NaN
     }
@@ -913,7 +928,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   }
 #pragma unroll
   for (int r = 0; r < kMaxOut; ++r) {
-    const int idx = threadIdx.x + 256 * r;
+    const int idx = threadIdx.x + kThreads * r;
     if (idx < nout) {
       const int h = idx / D, d = idx % D;
       out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num[r] / den_s[h]);
@@ -921,16 +936,17 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   }
 }
 
-// One workgroup per (live item, KV head). The KV heads of one (sequence,
-// split) are adjacent workgroups, so both halves of the same slot rows are
-// read at about the same time; the grid is sized for the widest table and the
-// workgroups past the live items exit after the context lengths.
-template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds>
-__global__ __launch_bounds__(256) void decode_mfma(DecodeParams p) {
+// One workgroup per (live item, kH KV heads). The KV-head groups of one
+// (sequence, split) are adjacent workgroups; the grid is sized for the widest
+// table and the workgroups past the live items exit after the context
+// lengths.
+template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH>
+__global__ __launch_bounds__(64 * kWaves * kH) void decode_mfma(DecodeParams p) {
   const int64_t cap = p.max_blocks * p.block_size;
-  const WorkItem it = find_item(p, blockIdx.x / p.hkv, cap);
+  const int nhg = p.hkv / kH;  // KV-head groups per item
+  const WorkItem it = find_item(p, blockIdx.x / nhg, cap);
   if (it.b < 0) return;  // uniform
-  decode_item<D, kBatch, kDouble, kAppend, kLds>(p, it, blockIdx.x % p.hkv);
+  decode_item<D, kBatch, kDouble, kAppend, kLds, kH>(p, it, (blockIdx.x % nhg) * kH);
 }
 
 }  // namespace
@@ -941,14 +957,15 @@ bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
          group >= 1 && group <= 16 && block_size % 16 == 0;
 }
 
-template <int D, int B, bool DB, bool A, bool L>
+template <int D, int B, bool DB, bool A, bool L, int H = 1>
 int launch_one(const DecodeParams &p, hipStream_t stream) {
-  // Every (sequence, split) item that can exist, times the KV heads.
-  const int64_t items = (int64_t)p.batch * p.max_splits * p.hkv;
+  // Every (sequence, split) item that can exist, times the KV-head groups.
+  const int64_t items = (int64_t)p.batch * p.max_splits * (p.hkv / H);
   if (items > 0x7fffffff)
     return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_decode: %lld work items exceed the grid",
                      (long long)items);
-  decode_mfma<D, B, DB, A, L><<<dim3(static_cast<unsigned>(items)), 256, 0, stream>>>(p);
+  decode_mfma<D, B, DB, A, L, H><<<dim3(static_cast<unsigned>(items)), 64 * kWaves * H, 0,
+                                   stream>>>(p);
   return check_launch("mlr_paged_decode(mfma)");
 }
 
@@ -963,9 +980,17 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
     if (tiles_per_wave <= 4)
       return append ? launch_one<64, 4, false, true, false>(p, stream)
                     : launch_one<64, 4, false, false, false>(p, stream);
-    if (p.ts == kLdsSplit64)
-      return append ? launch_one<64, 4, false, true, true>(p, stream)
-                    : launch_one<64, 4, false, false, true>(p, stream);
+    if (p.ts == kLdsSplit64) {
+      // Without the fused write, both KV heads of a pair go to one workgroup
+      // when their GQA groups fit the merge's 16 query-head rows (measured
+      // at batch 64 x 14/2 heads: 21.9 us against 22.2 us per step; with the
+      // write fused in, 22.4 us against 22.1 us, so that path keeps one KV
+      // head per workgroup).
+      if (append) return launch_one<64, 4, false, true, true>(p, stream);
+      if (p.hkv % 2 == 0 && 2 * p.group <= 16)
+        return launch_one<64, 4, false, false, true, 2>(p, stream);
+      return launch_one<64, 4, false, false, true>(p, stream);
+    }
     return append ? launch_one<64, 4, true, true, false>(p, stream)
                   : launch_one<64, 4, true, false, false>(p, stream);
   }

@@ -80,6 +80,8 @@ def test_fp32_decode_b4_with_new_token_write(device):
 CASES = [
     # (dtype, hq, hkv, d, block_size, seq_lens)
     (torch.bfloat16, 14, 2, 64, 16, [1, 15, 16, 17, 300, 1000]),   # MFMA, G=7
+    (torch.bfloat16, 16, 2, 64, 16, [100, 321, 640, 2000]),        # MFMA, KV pair, G=8
+    (torch.bfloat16, 16, 4, 64, 16, [5, 320, 1290]),               # MFMA, two KV pairs
     (torch.bfloat16, 28, 4, 128, 16, [33, 700, 2049]),             # MFMA, D=128
     (torch.bfloat16, 8, 8, 64, 16, [5, 100]),                      # MFMA, G=1
     (torch.bfloat16, 32, 2, 64, 32, [64, 513]),                    # MFMA, G=16, BS=32
