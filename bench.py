@@ -39,7 +39,8 @@ decodes + 2 x 1024-token prefills per step, 128 steps after the warm-up).
     python bench.py [--gpus 1] [--steps 240] [--warmup 48]
 
 ``--profile`` launches the same kernels eagerly and untimed, for rocprofv3:
-``--steps`` decode steps over the rotated layers, ten prefill calls, the
+``--steps`` decode steps over the rotated layers, one decode without the
+fused write per layer, the read floor per layer, ten prefill calls, the
 fused pre-attention kernel, and a plain 1 GiB device copy whose FETCH_SIZE /
 WRITE_SIZE counters calibrate the traffic counters (the copy reads and
 writes exactly 1 GiB).
@@ -192,12 +193,18 @@ def profile_run(args, device):
         k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
         kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, workspace=ws, new_k=new_k,
                                 new_v=new_v, slot_mapping=slots)
+    # The decode without the fused write (the served pair's decode; its own
+    # instantiation, one workgroup per pair of KV heads).
+    for i in range(LAYERS):
+        k_layer, v_layer = cache.get_layer_cache(i)
+        kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, workspace=ws)
     floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // 320), dtype=torch.int32, device=device)
     for i in range(LAYERS):
         k_layer, v_layer = cache.get_layer_cache(i)
         kpa.paged_kv_read_floor(k_layer, v_layer, bt, ctx, tokens_per_item=320, out=floor_out)
     torch.cuda.synchronize()
-    print(f"profile: {args.steps} decode steps, {LAYERS} read-floor passes", flush=True)
+    print(f"profile: {args.steps} decode steps, {LAYERS} decode-only steps, {LAYERS} read-floor "
+          "passes", flush=True)
     del cache
     if not args.no_prefill:
         pw = workloads.bf16_prefill_chunk512_x8()
