@@ -504,20 +504,27 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     return idx < p.max_blocks ? bt_row[idx] : int64_t(-1);
   };
   int64_t blk_raw = raw_block_id(lane);
-  // Fused KV write: the new token's slot and its K/V rows (wave 0, 16 bytes
-  // per lane) come with the prologue, so that staging them (LDS and cache,
-  // by the workgroup that holds the token) waits for no tile load.
+  const int64_t t1 = min<int64_t>(ctx, t0 + p.ts);
+  // Fused KV write: the new token (position ctx - 1) lives in the last tile of
+  // the last split, and the wave that owns that tile (tiles are dealt
+  // round-robin) takes the new K/V rows: their slot and rows (16 bytes per
+  // lane) come with the prologue, so staging them (LDS and cache) waits for no
+  // tile load, and as the same wave reads them back no barrier is needed.
+  const int64_t last_pos = ctx - 1;
+  const bool append_here = kAppend && last_pos >= t0 && last_pos < t1;
+  const int last_rel = static_cast<int>(last_pos - t0) & ~15;  // tile of ctx - 1
+  const int last_tok = static_cast<int>(last_pos - t0) & 15;   // its row
+  const bool new_owner = append_here && w == (last_rel >> 4) % kWaves;  // uniform
   __shared__ __align__(16) uint16_t new_row_s[kH][2 * D];
   const int64_t new_slot = kAppend ? p.new_slots[b] : -1;
   const bool new_is_v = lane >= D / 8;
   const int new_off = 8 * (new_is_v ? lane - D / 8 : lane);
   uint4 new_chunk = make_uint4(0, 0, 0, 0);
-  if (kAppend && w == 0 && lane < D / 4)
+  if (new_owner && lane < D / 4)
     new_chunk = *reinterpret_cast<const uint4 *>(
         static_cast<const uint16_t *>(new_is_v ? p.new_v : p.new_k) + b * p.new_sb +
         (int64_t)kvh * p.new_sh + new_off);
 
-  const int64_t t1 = min<int64_t>(ctx, t0 + p.ts);
   const int ntiles = static_cast<int>(ceil_div(t1 - t0, 16));
 
   // Q^T as the B operand: lane l holds Q[head l%16][32j + 8g .. +8).
@@ -554,19 +561,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   lo.v = ((4 * g * p.hkv + kvh) * D + VC * m16) * 2;
   lo.v_step = row_elems * 2;
   const int live = static_cast<int>(t1 - t0);
-  // Fused KV write: the new token (position ctx - 1) lives in the last tile of
-  // the last split. The wave that owns that tile stores the new K/V rows to
-  // slot new_slots[b] and, when that slot is the one position ctx - 1 maps to,
-  // uses the new rows in place of what it just read from the cache.
-  const int64_t last_pos = ctx - 1;
-  const bool append_here = kAppend && last_pos >= t0 && last_pos < t1;
-  const int last_rel = static_cast<int>(last_pos - t0) & ~15;  // tile of ctx - 1
-  const int last_tok = static_cast<int>(last_pos - t0) & 15;   // its row
-  // Wave 0 of the workgroup that holds the new token copies its K and V rows
-  // to slot new_slots[b] and to LDS (16 bytes per lane); the barrier publishes
-  // them. Called once, after the first batch of tile loads is issued.
+  // The owning wave stores the new K/V rows to slot new_slots[b] and to LDS,
+  // and, when that slot is the one position ctx - 1 maps to, uses them in
+  // place of what it read from the cache for that row. Called once, after
+  // the wave's first batch of tile loads is issued. LDS operations of one
+  // wave complete in order, so the wave's later reads of new_row_s see these
+  // writes.
   auto stage_new_row = [&]() {
-    if (w == 0 && lane < D / 4) {
+    if (new_owner && lane < D / 4) {
       *reinterpret_cast<uint4 *>(new_row_s[hs] + (new_is_v ? D : 0) + new_off) = new_chunk;
       const int64_t num_slots = p.num_blocks * p.block_size;
       if (new_slot >= 0 && new_slot < num_slots) {
@@ -575,7 +577,6 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         *reinterpret_cast<uint4 *>(dst) = new_chunk;
       }
     }
-    __syncthreads();
   };
   // Marks row last_tok of the new token's tile for substitution when the
   // new slot is the one position ctx - 1 maps to.
@@ -612,9 +613,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       compute_tile<D, kAppend>(st, buf[u], qf, scale, live, g, m16, new_row_s[hs]);
   };
 
-  // The workgroup holding the new token stages its rows once, after every
-  // wave's first batch of loads is in flight (all four waves pass the
-  // barrier, with or without tiles).
+  // The wave holding the new token stages its rows once, after its first
+  // batch of loads is in flight.
   if constexpr (kDouble) {
     // Next batch in flight while the current one computes.
     // Batches are issued whether or not they hold tiles (absent tiles read
@@ -981,15 +981,15 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
       return append ? launch_one<64, 4, false, true, false>(p, stream)
                     : launch_one<64, 4, false, false, false>(p, stream);
     if (p.ts == kLdsSplit64) {
-      // Without the fused write, both KV heads of a pair go to one workgroup
-      // when their GQA groups fit the merge's 16 query-head rows (measured
-      // at batch 64 x 14/2 heads: 21.9 us against 22.2 us per step; with the
-      // write fused in, 22.4 us against 22.1 us, so that path keeps one KV
-      // head per workgroup).
-      if (append) return launch_one<64, 4, false, true, true>(p, stream);
+      // Both KV heads of a pair go to one workgroup when their GQA groups fit
+      // the merge's 16 query-head rows (measured at batch 64 x 14/2 heads:
+      // 21.8 us against 22.2 us per step with the fused write, 21.9 against
+      // 22.2 without).
       if (p.hkv % 2 == 0 && 2 * p.group <= 16)
-        return launch_one<64, 4, false, false, true, 2>(p, stream);
-      return launch_one<64, 4, false, false, true>(p, stream);
+        return append ? launch_one<64, 4, false, true, true, 2>(p, stream)
+                      : launch_one<64, 4, false, false, true, 2>(p, stream);
+      return append ? launch_one<64, 4, false, true, true>(p, stream)
+                    : launch_one<64, 4, false, false, true>(p, stream);
     }
     return append ? launch_one<64, 4, true, true, false>(p, stream)
                   : launch_one<64, 4, true, false, false>(p, stream);
