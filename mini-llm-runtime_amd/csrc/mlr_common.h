@@ -31,6 +31,10 @@ void clear_error();
 // Reports a launch failure (bad grid, missing code object) as MLR_ERR_HIP.
 int check_launch(const char *what);
 
+// Compute units of the current device, queried once per device; 0 when the
+// query fails.
+int current_device_cus();
+
 // ---------------------------------------------------------------------------
 // Storage types. bf16 and fp16 are carried as raw 16-bit patterns so that the
 // kernels control every rounding step themselves.

@@ -1,4 +1,5 @@
 // Error plumbing and version query of libmlr_attn.so.
+#include <atomic>
 #include <string>
 
 #include "mlr_common.h"
@@ -28,6 +29,21 @@ int check_launch(const char *what) {
                      hipGetErrorString(err));
   }
   return MLR_OK;
+}
+
+int current_device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cus_of[kMaxDevices];  // 0: not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cus_of[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    // Threads that race here store the same value.
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cus_of[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 }  // namespace mlr

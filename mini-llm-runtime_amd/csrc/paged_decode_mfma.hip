@@ -975,17 +975,23 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
   // head_dim 64 a 320-token split lands its fifth tile per wave in LDS.
   const int tiles_per_wave = static_cast<int>(ceil_div(ceil_div(p.ts, 16), kWaves));
   const bool append = p.new_k != nullptr;
+  // Both KV heads of a pair go to one eight-wave workgroup when their GQA
+  // groups fit the merge's 16 query-head rows and the paired grid still has a
+  // workgroup for every CU. Measured: batch 64 x 14/2 heads, head_dim 64,
+  // 320-token splits: 21.8 us per step against 22.2 us (fused write), 21.9
+  // against 22.2 (decode only); 8 x 32K tokens, 28/4 heads, head_dim 128:
+  // 100.7 us against 107.8 us at 16 splits, 109.7 against 113.5 at 32, but
+  // 119.7 against 104.2 at 8 splits (128 paired workgroups for 256 CUs).
+  const int cus = current_device_cus();
+  const bool pairs = p.hkv % 2 == 0 && 2 * p.group <= 16 && cus > 0 &&
+                     (int64_t)p.batch * p.max_splits * (p.hkv / 2) >= cus;
   // Instantiations: head_dim x (one load batch | + LDS tile | double-buffered) x append.
   if (p.d == 64) {
     if (tiles_per_wave <= 4)
       return append ? launch_one<64, 4, false, true, false>(p, stream)
                     : launch_one<64, 4, false, false, false>(p, stream);
     if (p.ts == kLdsSplit64) {
-      // Both KV heads of a pair go to one workgroup when their GQA groups fit
-      // the merge's 16 query-head rows (measured at batch 64 x 14/2 heads:
-      // 21.8 us against 22.2 us per step with the fused write, 21.9 against
-      // 22.2 without).
-      if (p.hkv % 2 == 0 && 2 * p.group <= 16)
+      if (pairs)
         return append ? launch_one<64, 4, false, true, true, 2>(p, stream)
                       : launch_one<64, 4, false, false, true, 2>(p, stream);
       return append ? launch_one<64, 4, false, true, true>(p, stream)
@@ -993,6 +999,13 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
     }
     return append ? launch_one<64, 4, true, true, false>(p, stream)
                   : launch_one<64, 4, true, false, false>(p, stream);
+  }
+  if (pairs) {
+    if (tiles_per_wave <= 2)
+      return append ? launch_one<128, 2, false, true, false, 2>(p, stream)
+                    : launch_one<128, 2, false, false, false, 2>(p, stream);
+    return append ? launch_one<128, 2, true, true, false, 2>(p, stream)
+                  : launch_one<128, 2, true, false, false, 2>(p, stream);
   }
   if (tiles_per_wave <= 2)
     return append ? launch_one<128, 2, false, true, false>(p, stream)
