@@ -150,22 +150,14 @@ def test_decode_append_equals_write_then_decode(device, dtype, lens, tokens_per_
     assert max_abs(fused, want) <= TOL[dtype]
 
 
-# Enough (sequence, split) items that the launcher gives every workgroup a
-# pair of KV heads at head_dim 128: one load batch per wave at 128 tokens per
-# split, double-buffered at 176.
-PAIR128_LENS = [2000, 1, 17, 640, 1999, 129, 700, 1500, 33, 1024, 1100, 385]
-
-
-@pytest.mark.parametrize("tokens_per_split", [128, 176])
-def test_head_dim_128_kv_head_pairs(device, tokens_per_split):
-    """Head_dim 128, 28/4 heads: decode against the oracle, and the fused
-    write against write-then-decode (same cache bits, same output bits)."""
-    lens = PAIR128_LENS
-    q, kc, vc, bt, sl, tables = random_paged(lens, 28, 4, 128, 16, dtype=torch.bfloat16,
-                                             seed=13, fill=0.0)
-    gen = torch.Generator().manual_seed(7)
-    new_k = torch.randn(len(lens), 4, 128, generator=gen).bfloat16()
-    new_v = torch.randn(len(lens), 4, 128, generator=gen).bfloat16()
+def _fused_and_plain_vs_oracle(device, lens, hq, hkv, d, tokens_per_split, seed):
+    """The fused write against write-then-decode (same cache bits, same output
+    bits) and the decode against the oracle, BF16."""
+    q, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, 16, dtype=torch.bfloat16,
+                                             seed=seed, fill=0.0)
+    gen = torch.Generator().manual_seed(seed + 1)
+    new_k = torch.randn(len(lens), hkv, d, generator=gen).bfloat16()
+    new_v = torch.randn(len(lens), hkv, d, generator=gen).bfloat16()
     slots = torch.tensor([tables[b][(n - 1) // 16] * 16 + (n - 1) % 16
                           for b, n in enumerate(lens)])
     q, bt, sl, slots_d = (t.to(device) for t in (q, bt, sl, slots))
@@ -174,14 +166,43 @@ def test_head_dim_128_kv_head_pairs(device, tokens_per_split):
     nk, nv = new_k.to(device), new_v.to(device)
     fused = kpa.paged_decode_launch(q, k1, v1, bt, sl, new_k=nk, new_v=nv,
                                     slot_mapping=slots_d, tokens_per_split=tokens_per_split)
-    k2.view(-1, 4, 128).index_copy_(0, slots_d, nk)
-    v2.view(-1, 4, 128).index_copy_(0, slots_d, nv)
+    k2.view(-1, hkv, d).index_copy_(0, slots_d, nk)
+    v2.view(-1, hkv, d).index_copy_(0, slots_d, nv)
     plain = kpa.paged_decode_launch(q, k2, v2, bt, sl, tokens_per_split=tokens_per_split)
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
     assert torch.equal(fused, plain)
     want = opa.decode_batch_loop(q.cpu(), k2.cpu(), v2.cpu(), tables, lens, 16)
     assert torch.isfinite(plain).all()
     assert max_abs(plain, want) <= 2e-2
+
+
+# Enough (sequence, split) items that the launcher gives every workgroup a
+# pair of KV heads (batch x splits x Hkv/2 at least the GPU's 256 CUs).
+# Head_dim 128: one load batch per wave at 128 tokens per split,
+# double-buffered at 176.
+PAIR128_LENS = [2000, 1, 17, 640, 1999, 129, 700, 1500, 33, 1024, 1100, 385]
+
+
+@pytest.mark.parametrize("tokens_per_split", [128, 176])
+def test_head_dim_128_kv_head_pairs(device, tokens_per_split):
+    """Head_dim 128, 28/4 heads."""
+    _fused_and_plain_vs_oracle(device, PAIR128_LENS, 28, 4, 128, tokens_per_split, seed=13)
+
+
+# Head_dim 64 at the default 320-token splits (a fifth tile per wave in LDS):
+# 24 sequences up to 3520 tokens (11 splits) with one pair of KV heads, and
+# 12 with two pairs.
+PAIR64_LENS = [3520, 1, 16, 17, 321, 640, 641, 2999, 3201, 150, 1280, 2048,
+               900, 3333, 77, 2500, 319, 320, 1919, 3100, 2222, 1234, 555, 3456]
+
+
+@pytest.mark.parametrize("hq,hkv,lens", [
+    (16, 2, PAIR64_LENS),          # GQA group 8: the merge's 16 query-head rows full
+    (14, 2, PAIR64_LENS),          # Qwen2.5-0.5B heads
+    (16, 4, PAIR64_LENS[:12]),     # two KV-head pairs per item
+], ids=["16x2", "14x2", "16x4"])
+def test_head_dim_64_kv_head_pairs(device, hq, hkv, lens):
+    _fused_and_plain_vs_oracle(device, lens, hq, hkv, 64, 0, seed=29)
 
 
 def test_batch_permutation_is_bitwise_invariant(device):
