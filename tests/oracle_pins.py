@@ -118,9 +118,10 @@ def random_paged(seq_lens, hq, hkv, d, block_size, dtype=torch.float32, seed=0,
         tables.append(table)
         k = torch.randn(s, hkv, d, generator=gen).to(dtype)
         v = torch.randn(s, hkv, d, generator=gen).to(dtype)
-        for pos in range(s):
-            k_cache[table[pos // block_size], pos % block_size] = k[pos]
-            v_cache[table[pos // block_size], pos % block_size] = v[pos]
+        pos = torch.arange(s)
+        blocks = torch.tensor(table, dtype=torch.long)[pos // block_size]
+        k_cache[blocks, pos % block_size] = k
+        v_cache[blocks, pos % block_size] = v
     width = max(need)
     bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.long)
     q = torch.randn(len(seq_lens), hq, d, generator=gen).to(dtype)

@@ -205,6 +205,23 @@ def test_head_dim_64_kv_head_pairs(device, hq, hkv, lens):
     _fused_and_plain_vs_oracle(device, lens, hq, hkv, 64, 0, seed=29)
 
 
+# Seeded random batches of 24-40 sequences with contexts U[1, 4000] (plus a
+# 4000-token, a split-boundary and a one-token sequence), sized so the
+# launcher takes the KV-head-pair kernels: Qwen2.5-0.5B heads, GQA groups of
+# 8 and 4, two KV-head pairs per item (12/4), and head_dim 128.
+PAIR_SHAPES = [(14, 2, 64), (16, 2, 64), (8, 2, 64), (12, 4, 64), (28, 4, 128), (14, 2, 64)]
+
+
+@pytest.mark.parametrize("seed", range(len(PAIR_SHAPES)))
+def test_kv_head_pairs_random_batches(device, seed):
+    hq, hkv, d = PAIR_SHAPES[seed]
+    gen = torch.Generator().manual_seed(1000 + seed)
+    batch = int(torch.randint(24, 41, (1,), generator=gen))
+    lens = torch.randint(1, 4001, (batch,), generator=gen).tolist()
+    lens[:3] = [4000, 320 * (1 + seed % 3), 1]
+    _fused_and_plain_vs_oracle(device, lens, hq, hkv, d, 0, seed=200 + seed)
+
+
 def test_batch_permutation_is_bitwise_invariant(device):
     q, kc, vc, bt, sl, _ = random_paged([64, 129, 1024, 3000, 17], 14, 2, 64, 16,
                                         dtype=torch.bfloat16, seed=9)
