@@ -30,7 +30,7 @@
 // kBatch tiles at once and the next batch's loads before computing the
 // current one (two register buffers), so 8-16 KiB per wave are in flight.
 //
-// The four waves merge through LDS. A sequence that fits one split writes its
+// A KV head's four waves merge through LDS. A sequence that fits one split writes its
 // output directly; otherwise every split but the last stores its (m, l, acc)
 // to the workspace with device-coherent stores, each word encoded so that
 // zero means "not stored yet", and the workgroup of the last split (the
