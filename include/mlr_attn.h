@@ -168,6 +168,39 @@ int mlr_paged_decode_append(
     int64_t out_stride_h, void *stream);
 
 /*
+ * The decode step of Qwen2Attention.forward_decode_batch_with_cache after its
+ * QKV projection, in one launch: the rotary embedding of q and of the new
+ * key, the KV write and the paged decode.
+ *
+ * Replaces, per layer, Qwen2RotaryEmbedding + apply_rotary_pos_emb at
+ * position context_lens[b] - 1 (model/qwen2.py:125-209, called at :605-607),
+ * kv_cache.write_slots (:608-613) and paged_attention_decode_batch_parallel
+ * (:614-621; kernels/reference/paged_attention.py:178-254). Results equal
+ * mlr_qkv_rope_write (positions = context_lens - 1, no bias) followed by
+ * mlr_paged_decode bit for bit: the rotation rounds like the reference, each
+ * bf16 product and sum rounded once, cos and sin of the position rounded to
+ * bf16.
+ *   qkv      : [batch, (num_q_heads + 2 num_kv_heads) * head_dim], row stride
+ *              qkv_stride_b, heads in the order q, k, v: the output of the
+ *              projection (Qwen2QKVProjection, :211-236) with its bias,
+ *              16-byte aligned rows
+ *   inv_freq : FP32 [head_dim / 2], the rotary module's inverse frequencies
+ *   slot_mapping : int64 [batch], the slot of position context_lens[b] - 1
+ * Other arguments as for mlr_paged_decode. bf16 with head_dim 64 or 128, at
+ * most 16 query heads per KV head and block_size a multiple of 16 only (other
+ * shapes: MLR_ERR_INVALID; run mlr_qkv_rope_write, then mlr_paged_decode).
+ * No counterpart of its own in the reference: it fuses the calls above.
+ */
+int mlr_paged_decode_qkv(
+    const void *qkv, int64_t qkv_stride_b, const float *inv_freq,
+    void *k_cache, void *v_cache, int64_t num_blocks, int64_t block_size,
+    int64_t num_kv_heads, int64_t head_dim, const int64_t *block_tables,
+    int64_t block_table_stride, int64_t max_blocks_per_seq, const int64_t *context_lens,
+    const int64_t *slot_mapping, int64_t batch, int64_t num_q_heads, double scale,
+    int dtype, int64_t tokens_per_split, void *workspace, size_t workspace_bytes, void *out,
+    int64_t out_stride_b, int64_t out_stride_h, void *stream);
+
+/*
  * mlr_paged_decode_append without a workspace argument: the decode scratch
  * (split counters and partials) is an 8 MiB array the library keeps on each
  * GPU it runs on, so the call allocates nothing. It has no counterpart in the

@@ -40,6 +40,10 @@ struct DecodeParams {
   const int64_t *new_slots;
   void *kc_w;  // writable views of kc / vc
   void *vc_w;
+  // Fused rotary embedding (mlr_paged_decode_qkv; inv_freq == nullptr:
+  // none): q and the new K/V rows are the QKV projection's rows; q and the
+  // new K row are rotated for position context_lens[b] - 1.
+  const float *inv_freq;
 };
 
 // Workspace: a 256-byte flag region, then the split partials (m, l) and acc,

@@ -316,12 +316,15 @@ extern "C" size_t mlr_paged_decode_workspace_size(int64_t batch,
 
 namespace {
 
-// The new-token rows of mlr_paged_decode_append.
+// The new-token rows of mlr_paged_decode_append (and, for
+// mlr_paged_decode_qkv, the inverse frequencies of the fused rotary
+// embedding; inv_freq == nullptr: none).
 struct AppendArgs {
   const void *new_k;
   const void *new_v;
   int64_t sb, sh;
   const int64_t *slots;
+  const float *inv_freq = nullptr;
 };
 
 int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -426,6 +429,13 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
     const bool rows_aligned = (reinterpret_cast<uintptr_t>(app->new_k) & 15u) == 0 &&
                               (reinterpret_cast<uintptr_t>(app->new_v) & 15u) == 0 &&
                               app->sb % 8 == 0 && app->sh % 8 == 0;
+    if (app->inv_freq != nullptr) {
+      // The fused rotary embedding exists on the matrix-core kernel only.
+      MLR_REQUIRE(mfma && rows_aligned,
+                  "mlr_paged_decode_qkv: needs bf16, head_dim 64 or 128, at most 16 query "
+                  "heads per KV head, block_size a multiple of 16 and 16-byte aligned rows");
+      p.inv_freq = app->inv_freq;
+    }
     if (mfma && rows_aligned) {
       p.new_k = app->new_k;
       p.new_v = app->new_v;
@@ -492,6 +502,34 @@ extern "C" int mlr_paged_decode_append(
                     num_q_heads, scale, dtype, tokens_per_split, workspace,
                     workspace_bytes, out, out_stride_b, out_stride_h, stream,
                     &app);
+}
+
+extern "C" int mlr_paged_decode_qkv(
+    const void *qkv, int64_t qkv_stride_b, const float *inv_freq,
+    void *k_cache, void *v_cache, int64_t num_blocks, int64_t block_size,
+    int64_t num_kv_heads, int64_t head_dim, const int64_t *block_tables,
+    int64_t block_table_stride, int64_t max_blocks_per_seq, const int64_t *context_lens,
+    const int64_t *slot_mapping, int64_t batch, int64_t num_q_heads, double scale,
+    int dtype, int64_t tokens_per_split, void *workspace, size_t workspace_bytes, void *out,
+    int64_t out_stride_b, int64_t out_stride_h, void *stream) {
+  clear_error();
+  MLR_REQUIRE(qkv && inv_freq, "mlr_paged_decode_qkv: null qkv or inv_freq");
+  MLR_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0,
+              "mlr_paged_decode_qkv: head counts and head_dim must be > 0");
+  MLR_REQUIRE(qkv_stride_b >= (num_q_heads + 2 * num_kv_heads) * head_dim,
+              "mlr_paged_decode_qkv: qkv row stride smaller than its row");
+  const size_t esz = static_cast<size_t>(dtype_size(dtype));
+  MLR_REQUIRE(esz > 0, "mlr_paged_decode_qkv: unknown dtype %d", dtype);
+  const unsigned char *base = static_cast<const unsigned char *>(qkv);
+  AppendArgs app{base + esz * static_cast<size_t>(num_q_heads * head_dim),
+                 base + esz * static_cast<size_t>((num_q_heads + num_kv_heads) * head_dim),
+                 qkv_stride_b, head_dim, slot_mapping};
+  app.inv_freq = inv_freq;
+  return run_decode(qkv, qkv_stride_b, head_dim, k_cache, v_cache, num_blocks, block_size,
+                    num_kv_heads, head_dim, block_tables, block_table_stride,
+                    max_blocks_per_seq, context_lens, batch, num_q_heads, scale, dtype,
+                    tokens_per_split, workspace, workspace_bytes, out, out_stride_b,
+                    out_stride_h, stream, &app);
 }
 
 // ---------------------------------------------------------------------------

@@ -81,6 +81,28 @@ __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
 }
 
+__device__ __forceinline__ float bf16_elem(const uint4 &v, int e) {
+  const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
+  return bf16_bits_to_float((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// Rotary embedding of one (x[i], x[i + d/2]) pair in bf16 as the reference's
+// apply_rotary_pos_emb computes it (model/qwen2.py:125-209), operation by
+// operation: each product and the sum rounded to bf16 (nearest even), no
+// fused multiply-add; the roundings go two at a time through
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ void rope_pair(float x_lo, float x_hi, float c, float s,
+                                          float &o_lo, float &o_hi) {
+#pragma clang fp contract(off)
+  float a = x_lo * c, b = -x_hi * s;
+  float e = x_hi * c, f = x_lo * s;
+  bf16_round2(a, b);
+  bf16_round2(e, f);
+  o_lo = a + b;
+  o_hi = e + f;
+  bf16_round2(o_lo, o_hi);
+}
+
 // Butterfly steps across lanes l ^ 16 and l ^ 32 as VALU lane swaps
 // (v_permlane16_swap / v_permlane32_swap), not LDS permutes: after the swap
 // of x with itself, the two halves of the result hold x of both partners, in
@@ -524,6 +546,17 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     new_chunk = *reinterpret_cast<const uint4 *>(
         static_cast<const uint16_t *>(new_is_v ? p.new_v : p.new_k) + b * p.new_sb +
         (int64_t)kvh * p.new_sh + new_off);
+  // Fused rotary embedding (p.inv_freq set; fused write only): every wave
+  // puts cos and sin of the decode position ctx - 1 for the d/2 frequencies,
+  // rounded to bf16, in its own LDS row and rotates q and the new K row with
+  // them, as the fused pre-attention kernel does (qkv_rope.hip), once the
+  // tile loads are in flight. The frequency is loaded here, before the tile
+  // loads: memory loads complete in order, so a load issued after them
+  // could only be used once they had all landed.
+  const bool rope = kAppend && p.inv_freq != nullptr;  // uniform
+  __shared__ float rope_s[kWaves * kH][D];  // cos at [i], sin at [d/2 + i]
+  float rope_freq = 0.f;
+  if (rope && lane < D / 2) rope_freq = p.inv_freq[lane];
 
   const int ntiles = static_cast<int>(ceil_div(t1 - t0, 16));
 
@@ -531,6 +564,36 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   bf16x8_t qf[QK];
 #pragma unroll
   for (int j = 0; j < QK; ++j) qf[j] = __builtin_bit_cast(bf16x8_t, qraw[j]);
+  // Rotates the lane's q fragments: fragment j < QK/2 holds dims
+  // 32j + 8g + e (e < 8) and fragment j + QK/2 their partners d/2 further, so
+  // each pair is in one lane. LDS operations of one wave complete in order,
+  // so the wave reads back the cos/sin it has just written.
+  auto rotate_q = [&]() {
+    if (lane < D / 2) {
+      // sincosf shares one argument reduction between the two; its results
+      // are those of cosf and sinf.
+      float sn, cs;
+      sincosf(static_cast<float>(ctx - 1) * rope_freq, &sn, &cs);
+      bf16_round2(cs, sn);
+      rope_s[wave][lane] = cs;
+      rope_s[wave][D / 2 + lane] = sn;
+    }
+    if (!head_ok) return;  // columns past the group stay zero
+#pragma unroll
+    for (int j = 0; j < QK / 2; ++j) {
+      const int i0 = 32 * j + 8 * g;
+      float lo[8], hi[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        rope_pair(bf16_elem(qraw[j], e), bf16_elem(qraw[j + QK / 2], e), rope_s[wave][i0 + e],
+                  rope_s[wave][D / 2 + i0 + e], lo[e], hi[e]);
+      qf[j] = __builtin_bit_cast(bf16x8_t, make_uint4(bf16_pack2(lo[0], lo[1]), bf16_pack2(lo[2], lo[3]),
+                                                      bf16_pack2(lo[4], lo[5]), bf16_pack2(lo[6], lo[7])));
+      qf[j + QK / 2] =
+          __builtin_bit_cast(bf16x8_t, make_uint4(bf16_pack2(hi[0], hi[1]), bf16_pack2(hi[2], hi[3]),
+                                                  bf16_pack2(hi[4], hi[5]), bf16_pack2(hi[6], hi[7])));
+    }
+  };
 
   const uint16_t *kc = static_cast<const uint16_t *>(p.kc);
   const uint16_t *vc = static_cast<const uint16_t *>(p.vc);
@@ -567,14 +630,42 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // the wave's first batch of tile loads is issued. LDS operations of one
   // wave complete in order, so the wave's later reads of new_row_s see these
   // writes.
+  // With the fused rotary embedding each K lane takes the chunk of its
+  // rotary partner (K chunks of lanes l and l ^ d/16 hold dims i and
+  // i + d/2) and rotates its own, so the slot and LDS receive the finished
+  // rows.
   auto stage_new_row = [&]() {
-    if (new_owner && lane < D / 4) {
-      *reinterpret_cast<uint4 *>(new_row_s[hs] + (new_is_v ? D : 0) + new_off) = new_chunk;
+    if (!new_owner) return;  // uniform
+    uint4 v = new_chunk;
+    if (rope) {
+      uint4 xp;
+      xp.x = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v.x), D / 16, 64));
+      xp.y = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v.y), D / 16, 64));
+      xp.z = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v.z), D / 16, 64));
+      xp.w = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v.w), D / 16, 64));
+      if (!new_is_v) {
+        const bool low = new_off < D / 2;
+        const int i0 = low ? new_off : new_off - D / 2;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = bf16_elem(v, e), xo = bf16_elem(xp, e);
+          float ol, oh;
+          rope_pair(low ? x : xo, low ? xo : x, rope_s[wave][i0 + e],
+                    rope_s[wave][D / 2 + i0 + e], ol, oh);
+          o[e] = low ? ol : oh;
+        }
+        v = make_uint4(bf16_pack2(o[0], o[1]), bf16_pack2(o[2], o[3]), bf16_pack2(o[4], o[5]),
+                       bf16_pack2(o[6], o[7]));
+      }
+    }
+    if (lane < D / 4) {
+      *reinterpret_cast<uint4 *>(new_row_s[hs] + (new_is_v ? D : 0) + new_off) = v;
       const int64_t num_slots = p.num_blocks * p.block_size;
       if (new_slot >= 0 && new_slot < num_slots) {
         uint16_t *dst = static_cast<uint16_t *>(new_is_v ? p.vc_w : p.kc_w) +
                         (new_slot * p.hkv + kvh) * D + new_off;
-        *reinterpret_cast<uint4 *>(dst) = new_chunk;
+        *reinterpret_cast<uint4 *>(dst) = v;
       }
     }
   };
@@ -621,6 +712,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     // zeros), so the wait before each compute counts only its own batch.
     Tile<D> bufA[kBatch], bufB[kBatch];
     issue(bufA, 0);
+    if (rope) rotate_q();
     if (append_here) stage_new_row();
     for (int kb = 0; kb < nk; kb += 2 * kBatch) {
       issue(bufB, kb + kBatch);
@@ -643,6 +735,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     copy_tile_to_lds(lds_tiles[wave], kc, vc, block_elems,
                      static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel4)) * row_elems * 2,
                      blk4, kvh, row_elems * 2, lane);
+    if (rope) rotate_q();
     if (append_here) stage_new_row();
     compute(buf);
     if (kBatch < nk) {  // uniform
@@ -655,6 +748,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     // reaching the computes has the same loads in flight.
     Tile<D> buf[kBatch];
     issue(buf, 0);
+    if (rope) rotate_q();
     if (append_here) stage_new_row();
     for (int kb = 0; kb < nk; kb += kBatch) {
       if (kb > 0) issue(buf, kb);

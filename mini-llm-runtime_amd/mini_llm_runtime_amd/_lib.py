@@ -61,6 +61,12 @@ _PROTOTYPES = {
          _c_int, _c_i64, _c_ptr, _c_size, _c_ptr, _c_ptr, _c_i64, _c_i64,
          _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr],
     ),
+    "mlr_paged_decode_qkv": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_f64,
+         _c_int, _c_i64, _c_ptr, _c_size, _c_ptr, _c_i64, _c_i64, _c_ptr],
+    ),
     "mlr_paged_decode_append_static": (
         _c_int,
         [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64,

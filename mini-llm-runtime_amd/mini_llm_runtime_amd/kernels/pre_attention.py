@@ -8,6 +8,10 @@ replaces the reference's per-layer sequence Qwen2RotaryEmbedding ->
 apply_rotary_pos_emb -> kv_cache.write_slots (model/qwen2.py:125-209,
 :605-613, :737-746), with the same rounding in the model dtype.
 
+``qkv_rope_decode`` goes one step further for a decode step: the same
+rotation and KV write and the batched paged decode in one launch
+(``mlr_paged_decode_qkv``).
+
 Checks are on shapes, dtypes and devices only; slot values are the caller's
 to validate (``PagedKVCache.check_slots`` runs the reference's write_slots
 checks). A slot outside the pool is not written.
@@ -19,6 +23,7 @@ import torch
 
 from .. import _lib
 from ..runtime.paged_kv_cache import PagedKVCache
+from . import paged_attention as kpa
 
 _SUPPORTED = (torch.float32, torch.float16, torch.bfloat16)
 
@@ -106,4 +111,91 @@ def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, inv_freq: torch.T
             tokens, num_q_heads, hkv, d, _lib.dtype_code(qkv.dtype, "qkv_rope_write"),
             _lib.stream_handle(device))
     _lib.check(status, "mlr_qkv_rope_write")
+    return out
+
+
+def qkv_rope_decode_fusable(qkv_dtype: torch.dtype, kv_cache: PagedKVCache,
+                            num_q_heads: int) -> bool:
+    """Shapes ``qkv_rope_decode`` covers: bf16, head_dim 64 or 128, at most 16
+    query heads per KV head, block_size a multiple of 16, the cache in the
+    model dtype. Other shapes run qkv_rope_write and then the decode."""
+    hkv = kv_cache.num_kv_heads
+    return (qkv_dtype == torch.bfloat16 and kv_cache.dtype == torch.bfloat16
+            and kv_cache.head_dim in (64, 128) and num_q_heads % hkv == 0
+            and 0 < num_q_heads // hkv <= 16 and kv_cache.block_size % 16 == 0)
+
+
+def qkv_rope_decode(qkv: torch.Tensor, inv_freq: torch.Tensor, kv_cache: PagedKVCache,
+                    layer_idx: int, slot_mapping: torch.Tensor, block_tables: torch.Tensor,
+                    context_lens: torch.Tensor, num_q_heads: int, *,
+                    out: torch.Tensor | None = None,
+                    scale: float | None = None, tokens_per_split: int = 0,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode step of a layer after its QKV projection, in one launch
+    (``mlr_paged_decode_qkv``): qkv [B, (Hq + 2 Hkv) * D], the projection's
+    output with its bias -> attention output [B, Hq, D]; the rotated k and v
+    of each request are written to slot_mapping[b] of the layer's cache on
+    the way.
+
+    Each request's token sits at position context_lens[b] - 1 and
+    slot_mapping[b] is that position's slot; the caller validates this
+    metadata (Qwen2Attention does, with the reference's checks). Results equal
+    ``qkv_rope_write`` at those positions (without its bias) followed by the
+    batched decode bit for bit. Only shapes ``qkv_rope_decode_fusable`` accepts.
+    """
+    if layer_idx < 0 or layer_idx >= kv_cache.num_layers:
+        raise IndexError("Unexpected layer_idx")
+    hkv, d = kv_cache.num_kv_heads, kv_cache.head_dim
+    if not qkv_rope_decode_fusable(qkv.dtype, kv_cache, num_q_heads):
+        raise ValueError("qkv_rope_decode needs bf16, head_dim 64 or 128, at most 16 query "
+                         "heads per KV head and a block_size multiple of 16")
+    width = (num_q_heads + 2 * hkv) * d
+    if qkv.ndim != 2 or qkv.shape[1] != width or qkv.shape[0] == 0:
+        raise ValueError(f"qkv must have shape [batch, {width}] with batch > 0, "
+                         f"got {tuple(qkv.shape)}")
+    batch = qkv.shape[0]
+    if qkv.stride(1) != 1 or qkv.stride(0) % 8 != 0:
+        qkv = qkv.contiguous()
+    if inv_freq.shape != (d // 2,):
+        raise ValueError(f"inv_freq must have shape [{d // 2}]")
+    for name, tensor in (("slot_mapping", slot_mapping), ("context_lens", context_lens)):
+        if tensor.shape != (batch,) or tensor.dtype != torch.long:
+            raise ValueError(f"{name} must be an int64 tensor of shape [batch]")
+    if (block_tables.ndim != 2 or block_tables.shape[0] != batch
+            or block_tables.dtype != torch.long):
+        raise ValueError("block_tables must be an int64 tensor of shape [batch, max_blocks]")
+    device = _lib.require_hip(qkv, inv_freq, slot_mapping, context_lens, block_tables,
+                              kv_cache.k_cache, what="qkv_rope_decode")
+    layer_k, layer_v = kv_cache.get_layer_cache(layer_idx)
+    if not (layer_k.is_contiguous() and layer_v.is_contiguous()):
+        raise ValueError("KV cache layers must be contiguous")
+    if out is None:
+        out = torch.empty((batch, num_q_heads, d), dtype=qkv.dtype, device=device)
+    elif out.shape != (batch, num_q_heads, d) or out.dtype != qkv.dtype or out.stride(2) != 1:
+        raise ValueError("out must be [batch, num_q_heads, head_dim] with contiguous rows")
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    slot_mapping, context_lens = slot_mapping.contiguous(), context_lens.contiguous()
+    freq = _freq_fp32(inv_freq)
+    width_blocks = block_tables.shape[1]
+    if scale is None:
+        scale = d ** -0.5
+    dcode = _lib.dtype_code(qkv.dtype, "qkv_rope_decode")
+    lib = _lib.load()
+    ws_bytes = int(lib.mlr_paged_decode_workspace_size(
+        batch, num_q_heads, d, width_blocks * kv_cache.block_size, tokens_per_split, dcode))
+    if workspace is None:
+        workspace = kpa.decode_workspace(device, ws_bytes)
+    elif workspace.numel() < ws_bytes:
+        raise ValueError(f"decode workspace of {workspace.numel()} bytes is smaller than "
+                         f"the {ws_bytes} bytes required")
+    with torch.cuda.device(device):
+        status = lib.mlr_paged_decode_qkv(
+            qkv.data_ptr(), qkv.stride(0), freq.data_ptr(), layer_k.data_ptr(), layer_v.data_ptr(), kv_cache.num_blocks,
+            kv_cache.block_size, hkv, d, block_tables.data_ptr(), block_tables.stride(0),
+            width_blocks, context_lens.data_ptr(), slot_mapping.data_ptr(), batch,
+            num_q_heads, float(scale), dcode, int(tokens_per_split), workspace.data_ptr(),
+            workspace.numel(), out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.stream_handle(device))
+    _lib.check(status, "mlr_paged_decode_qkv")
     return out

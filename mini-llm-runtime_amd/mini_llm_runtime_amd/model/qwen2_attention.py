@@ -14,7 +14,9 @@ the reference's rounding; then the attention kernel:
 - ``forward_decode_batch_with_cache`` validates the step's metadata with one
   host sync, then runs the fused step and the batched decode, replacing the
   write_slots + paged_attention_decode_batch_parallel pair (reference
-  :608-621).
+  :608-621). For bf16 with head_dim 64 or 128 the rotation, the KV write and
+  the decode are a single ``mlr_paged_decode_qkv`` launch after the
+  projection; the results are the same bit for bit.
 - ``forward_prefill_packed_with_cache`` (all prefill requests of a step) runs
   the fused step and one varlen prefill.
 - ``forward_prefill_chunk_with_cache`` runs the fused step and the tiled
@@ -362,9 +364,17 @@ class Qwen2Attention(nn.Module):
             raise ValueError("KV cache dtype must match hidden_states dtype")
         self._check_decode_metadata(kv_cache, position_ids, slot_mapping, block_tables,
                                     context_lens)
-        k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)
         # The metadata checks above are the ones write_slots and the decode
         # would repeat.
+        if kpre.qkv_rope_decode_fusable(hidden_states.dtype, kv_cache, self.num_attention_heads):
+            # Rotation, KV write and decode in one launch after the projection.
+            weight, bias = self._qkv_weights()
+            qkv = torch.nn.functional.linear(hidden_states[:, 0], weight, bias)
+            out = kpre.qkv_rope_decode(qkv, self.rotary_embedding.inv_freq, kv_cache,
+                                       layer_idx, slot_mapping, block_tables, context_lens,
+                                       self.num_attention_heads)
+            return self.o_proj(out.reshape(batch, 1, self.hidden_size))
+        k_layer, v_layer = kv_cache.get_layer_cache(layer_idx)
         query = self._fused_qkv_rope_write(hidden_states[:, 0], position_ids[:, 0], kv_cache,
                                            layer_idx, slot_mapping)
         out = kpa.paged_decode_launch(query, k_layer, v_layer, block_tables, context_lens)

@@ -80,6 +80,15 @@ def test_workspace_size_is_host_arithmetic():
     (lambda lib: lib.mlr_paged_prefill(None, 0, 0, None, None, 8, 16, 2, 300, None, 4, 4,
                                        None, None, 1, 4, 14, 0.125, 2, 64, None, 0, 0,
                                        None), b"head_dim"),
+    (lambda lib: lib.mlr_paged_decode_qkv(None, 1152, None, None, None, 8, 16, 2, 64,
+                                          None, 4, 4, None, None, 2, 14, 0.125, 2, 0, None,
+                                          0, None, 0, 0, None), b"null qkv or inv_freq"),
+    # FP32 has no fused rotary path: refused on the host, before any launch
+    # (the device pointers are never dereferenced).
+    (lambda lib: lib.mlr_paged_decode_qkv(1 << 12, 1152, 1 << 13, 1 << 20, 1 << 21, 8,
+                                          16, 2, 64, 1 << 22, 4, 4, 1 << 23, 1 << 24, 2, 14,
+                                          0.125, 0, 0, 1 << 25, 1 << 30, 1 << 26, 896, 64,
+                                          None), b"needs bf16"),
 ])
 def test_argument_errors_return_before_any_launch(call, needle):
     lib = _lib.load()

@@ -1,0 +1,152 @@
+"""One-launch decode step (mlr_paged_decode_qkv: rotary embedding of q and the
+new key + KV write + paged decode after the QKV projection) on the GPU.
+
+The fused call must equal the two launches it replaces bit for bit: the
+pre-attention step mlr_qkv_rope_write at positions context_lens - 1 (itself
+bit-exact against the reference's PyTorch rotation and checked against the
+oracle in test_gpu_pre_attention.py), then the batched decode. Both the
+output and the cache rows written are compared with torch.equal, and the
+decode output is checked against the oracle's decode (max-abs 2e-2, BF16
+inputs with FP32 softmax). The cases reach every kernel layout the launcher
+picks: head_dim 64 with one load batch per wave, a fifth tile in LDS (one KV
+head or a pair per workgroup) and double-buffered loads; head_dim 128 with one
+or two load batches per wave, with and without KV-head pairs.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle.paged_attention as opa
+from mini_llm_runtime_amd.kernels import paged_attention as kpa
+from mini_llm_runtime_amd.kernels import pre_attention as kpre
+from mini_llm_runtime_amd.model.qwen2_attention import Qwen2RotaryEmbedding
+from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+from oracle_pins import random_paged
+
+pytestmark = pytest.mark.gpu
+
+THETA = 1_000_000.0
+BS = 16
+
+# Contexts that give 24 sequences enough (sequence, split) items for the
+# KV-head-pair kernels at head_dim 64 (320-token splits) and 128.
+LENS64 = [3520, 1, 16, 17, 321, 640, 641, 2999, 3201, 150, 1280, 2048,
+          900, 3333, 77, 2500, 319, 320, 1919, 3100, 2222, 1234, 555, 3456]
+LENS128 = [2000, 1, 17, 640, 1999, 129, 700, 1500, 33, 1024, 1100, 385]
+
+CASES = [
+    # (id, hq, hkv, d, lens, tokens_per_split)
+    ("d64-one-batch", 14, 2, 64, [1, 16, 17, 300, 1000, 257], 64),
+    ("d64-lds-tile", 14, 2, 64, [300, 384, 770, 5, 321, 640], 320),
+    ("d64-lds-pairs", 14, 2, 64, LENS64, 0),
+    ("d64-lds-pairs-g8", 16, 2, 64, LENS64, 320),
+    ("d64-double", 16, 4, 64, [300, 384, 770, 5, 1500], 384),
+    ("d64-mha", 8, 8, 64, [33, 64, 500, 2000], 0),
+    ("d64-group16", 32, 2, 64, [1, 700, 2100], 0),
+    ("d128-one-batch", 8, 1, 128, [5, 129, 700, 64], 64),
+    ("d128-double", 16, 1, 128, [5, 129, 700, 64, 1000], 176),
+    ("d128-pairs", 28, 4, 128, LENS128, 128),
+    ("d128-pairs-double", 28, 4, 128, LENS128, 176),
+]
+
+
+def _case(hq, hkv, d, lens, seed):
+    _, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, BS, dtype=torch.bfloat16,
+                                             seed=seed, fill=0.0)
+    gen = torch.Generator().manual_seed(seed + 7)
+    qkv = torch.randn(len(lens), (hq + 2 * hkv) * d, generator=gen).bfloat16()
+    slots = torch.tensor([tables[b][(n - 1) // BS] * BS + (n - 1) % BS
+                          for b, n in enumerate(lens)])
+    return qkv, kc, vc, bt, sl, slots, tables
+
+
+def _cache(kc, vc, device):
+    nb, bs, hkv, d = kc.shape
+    cache = PagedKVCache(1, nb, bs, hkv, d, dtype=kc.dtype, device=device)
+    cache.k_cache[0].copy_(kc)
+    cache.v_cache[0].copy_(vc)
+    return cache
+
+
+def _two_launches(qkv, inv_freq, cache, bt, sl, slots, hq, tokens_per_split):
+    q = kpre.qkv_rope_write(qkv, sl - 1, inv_freq, cache, 0, slots, hq)
+    k, v = cache.get_layer_cache(0)
+    return kpa.paged_decode_launch(q, k, v, bt, sl, tokens_per_split=tokens_per_split), q
+
+
+@pytest.mark.parametrize("cid,hq,hkv,d,lens,tokens_per_split", CASES,
+                         ids=[c[0] for c in CASES])
+def test_one_launch_equals_rope_write_then_decode(device, cid, hq, hkv, d, lens,
+                                                  tokens_per_split):
+    qkv, kc, vc, bt, sl, slots, tables = _case(hq, hkv, d, lens, seed=len(lens) * 31 + d + hq)
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
+    qkv, bt, sl, slots = (t.to(device) for t in (qkv, bt, sl, slots))
+
+    two_cache = _cache(kc, vc, device)
+    want, q = _two_launches(qkv, inv_freq, two_cache, bt, sl, slots, hq, tokens_per_split)
+    one_cache = _cache(kc, vc, device)
+    got = kpre.qkv_rope_decode(qkv, inv_freq, one_cache, 0, slots, bt, sl, hq,
+                               tokens_per_split=tokens_per_split)
+    assert torch.equal(one_cache.k_cache, two_cache.k_cache)
+    assert torch.equal(one_cache.v_cache, two_cache.v_cache)
+    assert torch.equal(got, want)
+
+    k, v = two_cache.get_layer_cache(0)
+    oracle = opa.decode_batch_loop(q.cpu(), k.cpu(), v.cpu(), tables, lens, BS)
+    assert torch.isfinite(got).all()
+    assert (got.double().cpu() - oracle.double()).abs().max().item() <= 2e-2
+
+
+def test_bf16_inv_freq_and_strided_qkv_rows(device):
+    """A model cast to bf16 holds inv_freq in bf16 (used as its FP32 value, as
+    qkv_rope_write does), and qkv rows may come from a wider buffer."""
+    hq, hkv, d, lens = 14, 2, 64, [40, 1, 333]
+    qkv, kc, vc, bt, sl, slots, _ = _case(hq, hkv, d, lens, seed=3)
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device, torch.bfloat16)
+    wide = torch.zeros(len(lens), qkv.shape[1] + 64, dtype=torch.bfloat16)
+    wide[:, :qkv.shape[1]] = qkv
+    wide, bt, sl, slots = (t.to(device) for t in (wide, bt, sl, slots))
+    rows = wide[:, :qkv.shape[1]]
+
+    two_cache = _cache(kc, vc, device)
+    want, _ = _two_launches(rows.contiguous(), inv_freq, two_cache, bt, sl, slots, hq, 0)
+    one_cache = _cache(kc, vc, device)
+    got = kpre.qkv_rope_decode(rows, inv_freq, one_cache, 0, slots, bt, sl, hq)
+    assert torch.equal(one_cache.k_cache, two_cache.k_cache)
+    assert torch.equal(one_cache.v_cache, two_cache.v_cache)
+    assert torch.equal(got, want)
+
+
+def test_repeated_steps_reuse_the_workspace(device):
+    """Three decode steps in a row on one cache: each step's new row is read
+    back by the next, and the shared workspace is left clean each time."""
+    hq, hkv, d = 14, 2, 64
+    lens = [300, 17, 1000, 64]
+    qkv, kc, vc, bt, sl, _, tables = _case(hq, hkv, d, [n + 3 for n in lens], seed=11)
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
+    bt = bt.to(device)
+    one_cache, two_cache = _cache(kc, vc, device), _cache(kc, vc, device)
+    gen = torch.Generator().manual_seed(12)
+    for step in range(3):
+        ctx = torch.tensor([n + step + 1 for n in lens])
+        slots = torch.tensor([tables[b][(n - 1) // BS] * BS + (n - 1) % BS
+                              for b, n in enumerate(ctx.tolist())])
+        qkv = torch.randn(len(lens), qkv.shape[1], generator=gen).bfloat16().to(device)
+        ctx, slots = ctx.to(device), slots.to(device)
+        want, _ = _two_launches(qkv, inv_freq, two_cache, bt, ctx, slots, hq, 0)
+        got = kpre.qkv_rope_decode(qkv, inv_freq, one_cache, 0, slots, bt, ctx, hq)
+        assert torch.equal(got, want), step
+    assert torch.equal(one_cache.k_cache, two_cache.k_cache)
+    assert torch.equal(one_cache.v_cache, two_cache.v_cache)
+
+
+def test_shapes_outside_the_kernel_are_rejected(device):
+    cache = PagedKVCache(1, 8, BS, 2, 32, dtype=torch.bfloat16, device=device)
+    assert not kpre.qkv_rope_decode_fusable(torch.bfloat16, cache, 4)
+    qkv = torch.zeros(1, 8 * 32, dtype=torch.bfloat16, device=device)
+    one = torch.ones(1, dtype=torch.long, device=device)
+    with pytest.raises(ValueError, match="head_dim 64 or 128"):
+        kpre.qkv_rope_decode(qkv, torch.ones(16, device=device), cache, 0, one - 1,
+                             torch.zeros(1, 1, dtype=torch.long, device=device), one, 4)

@@ -317,6 +317,32 @@ def test_qkv_rope_write_refuses_cpu_tensors():
     assert torch.all(args["kv_cache"].k_cache == 5)
 
 
+def test_qkv_rope_decode_checks_shape_then_device():
+    from mini_llm_runtime_amd.kernels.pre_attention import (qkv_rope_decode,
+                                                            qkv_rope_decode_fusable)
+    from mini_llm_runtime_amd.model.qwen2_attention import Qwen2RotaryEmbedding
+    ctx = torch.tensor([3, 20])
+    tables = torch.tensor([[0, -1], [1, 2]])
+    slots = torch.tensor([2, 35])
+    fp32 = PagedKVCache(1, 4, 16, 2, 64, dtype=torch.float32)
+    assert not qkv_rope_decode_fusable(torch.float32, fp32, 14)
+    with pytest.raises(ValueError, match="needs bf16"):
+        qkv_rope_decode(torch.randn(2, 18 * 64), Qwen2RotaryEmbedding(64).inv_freq, fp32, 0,
+                        slots, tables, ctx, 14)
+    cache = PagedKVCache(1, 4, 16, 2, 64, dtype=torch.bfloat16)
+    assert qkv_rope_decode_fusable(torch.bfloat16, cache, 14)
+    assert not qkv_rope_decode_fusable(torch.bfloat16, cache, 34)  # 17 heads per KV head
+    cache.k_cache.fill_(5)
+    qkv = torch.randn(2, 18 * 64).bfloat16()
+    with pytest.raises(ValueError, match="qkv must have shape"):
+        qkv_rope_decode(qkv[:, :-8], Qwen2RotaryEmbedding(64).inv_freq, cache, 0, slots,
+                        tables, ctx, 14)
+    with pytest.raises(RuntimeError, match="only on HIP devices"):
+        qkv_rope_decode(qkv, Qwen2RotaryEmbedding(64).inv_freq, cache, 0, slots, tables,
+                        ctx, 14)
+    assert torch.all(cache.k_cache == 5)
+
+
 @pytest.mark.parametrize("p,v,error,message", [
     (torch.randn(2, 64), torch.randn(2, 64, 256), ValueError, "CUDA tensors"),
 ])
