@@ -22,9 +22,31 @@
 namespace mlr {
 namespace {
 
+// x rounded to T (nearest even) and back to FP32, for the intermediate
+// roundings; stored values go through Elem<T>::from_f32, which also maps
+// every NaN to the canonical one. bf16 rounds with v_cvt_pk_bf16_f32, two
+// values per instruction in rnd2.
 template <typename T>
 __device__ __forceinline__ float rnd(float x) {
   return Elem<T>::to_f32(Elem<T>::from_f32(x));
+}
+template <>
+__device__ __forceinline__ float rnd<bf16_t>(float x) {
+  return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(x)))
+                         << 16);
+}
+template <typename T>
+__device__ __forceinline__ void rnd2(float &a, float &b) {
+  a = rnd<T>(a);
+  b = rnd<T>(b);
+}
+template <>
+__device__ __forceinline__ void rnd2<bf16_t>(float &a, float &b) {
+  typedef float f32x2_v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{a, b}, bf16x2_v));
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
 }
 
 template <typename T>
@@ -85,15 +107,21 @@ __global__ __launch_bounds__(64) void qkv_rope_write_kernel(
         hi[k] = *reinterpret_cast<const V *>(row + (rope ? elo[k] + half : elo[k]));
       }
       if (c0 == 0) {
+        // sincosf: one argument reduction for both; its results are those
+        // of cosf and sinf.
         if (lane < half) {
-          const float f = pos * my_freq;
-          cs[lane] = rnd<T>(cosf(f));
-          cs[half + lane] = rnd<T>(sinf(f));
+          float sv, cv;
+          sincosf(pos * my_freq, &sv, &cv);
+          rnd2<T>(cv, sv);
+          cs[lane] = cv;
+          cs[half + lane] = sv;
         }
         for (int i = lane + 64; i < half; i += 64) {  // head_dim > 128
-          const float f = pos * inv_freq[i];
-          cs[i] = rnd<T>(cosf(f));
-          cs[half + i] = rnd<T>(sinf(f));
+          float sv, cv;
+          sincosf(pos * inv_freq[i], &sv, &cv);
+          rnd2<T>(cv, sv);
+          cs[i] = cv;
+          cs[half + i] = sv;
         }
         __syncthreads();
       }
@@ -112,8 +140,11 @@ __global__ __launch_bounds__(64) void qkv_rope_write_kernel(
               x_hi = rnd<T>(x_hi + load_f(bias + h * d + half + i0 + j));
             }
             const float cv = cs[i0 + j], sv = cs[half + i0 + j];
-            olo.v[j] = Elem<T>::from_f32(rnd<T>(rnd<T>(x_lo * cv) + rnd<T>(-x_hi * sv)));
-            ohi.v[j] = Elem<T>::from_f32(rnd<T>(rnd<T>(x_hi * cv) + rnd<T>(x_lo * sv)));
+            float a = x_lo * cv, b = -x_hi * sv, e = x_hi * cv, f = x_lo * sv;
+            rnd2<T>(a, b);
+            rnd2<T>(e, f);
+            olo.v[j] = Elem<T>::from_f32(a + b);
+            ohi.v[j] = Elem<T>::from_f32(e + f);
           }
           T *o = h < hq ? q_out + t * q_st + static_cast<int64_t>(h) * d
                         : kc + (slot * hkv + (h - hq)) * d;
@@ -127,8 +158,8 @@ __global__ __launch_bounds__(64) void qkv_rope_write_kernel(
           if (bias != nullptr) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j)
-              ov.v[j] = Elem<T>::from_f32(
-                  rnd<T>(Elem<T>::to_f32(lo[k].v[j]) + load_f(bias + v_base + ev + j)));
+              ov.v[j] = Elem<T>::from_f32(Elem<T>::to_f32(lo[k].v[j]) +
+                                          load_f(bias + v_base + ev + j));
           }
           *reinterpret_cast<V *>(vc + slot * hkv * d + ev) = ov;
         }
