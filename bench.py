@@ -42,7 +42,8 @@ decodes + 2 x 1024-token prefills per step, 128 steps after the warm-up).
 
 ``--profile`` launches the same kernels eagerly and untimed, for rocprofv3:
 ``--steps`` decode steps over the rotated layers, one decode without the
-fused write per layer, the read floor per layer, ten prefill calls, the
+fused write and one one-launch served step per layer, the read floor per
+layer, ten prefill calls, the
 fused pre-attention kernel, and a plain 1 GiB device copy whose FETCH_SIZE /
 WRITE_SIZE counters calibrate the traffic counters (the copy reads and
 writes exactly 1 GiB).
@@ -195,18 +196,28 @@ def profile_run(args, device):
         k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
         kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, workspace=ws, new_k=new_k,
                                 new_v=new_v, slot_mapping=slots)
-    # The decode without the fused write (the served pair's decode; its own
-    # instantiation, one workgroup per pair of KV heads).
+    # The decode without the fused write (the two-launch step's decode; its
+    # own instantiation, one workgroup per pair of KV heads).
     for i in range(LAYERS):
         k_layer, v_layer = cache.get_layer_cache(i)
         kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, workspace=ws)
+    # The served step in one launch (rotary embedding + KV write + decode:
+    # mlr_paged_decode_qkv, its own instantiation).
+    from mini_llm_runtime_amd.kernels import pre_attention as kpre
+    from mini_llm_runtime_amd.model.qwen2_attention import Qwen2RotaryEmbedding
+    gen = torch.Generator().manual_seed(64)
+    qkv = torch.randn(64, 18 * 64, generator=gen).to(torch.bfloat16).to(device)
+    inv_freq = Qwen2RotaryEmbedding(64, 1_000_000.0).inv_freq.to(device)
+    for i in range(LAYERS):
+        kpre.qkv_rope_decode(qkv, inv_freq, cache, i % LAYERS, slots, bt, ctx, 14, out=out,
+                             workspace=ws)
     floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // 320), dtype=torch.int32, device=device)
     for i in range(LAYERS):
         k_layer, v_layer = cache.get_layer_cache(i)
         kpa.paged_kv_read_floor(k_layer, v_layer, bt, ctx, tokens_per_item=320, out=floor_out)
     torch.cuda.synchronize()
-    print(f"profile: {args.steps} decode steps, {LAYERS} decode-only steps, {LAYERS} read-floor "
-          "passes", flush=True)
+    print(f"profile: {args.steps} decode steps, {LAYERS} decode-only steps, {LAYERS} one-launch "
+          f"served steps, {LAYERS} read-floor passes", flush=True)
     del cache
     if not args.no_prefill:
         pw = workloads.bf16_prefill_chunk512_x8()
@@ -967,8 +978,9 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": ("mlr_paged_decode_append (decode_mfma<64,4,false,true,true>: 320-token "
-                       "splits, KV write folded in, splits merged in the same launch)"),
+            "kernel": ("mlr_paged_decode_append (decode_mfma<64,4,false,true,true,2,false>: "
+                       "320-token splits, a pair of KV heads per workgroup, KV write folded "
+                       "in, splits merged in the same launch)"),
             "achieved": round(dec["value_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

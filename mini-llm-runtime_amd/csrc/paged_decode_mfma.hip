@@ -478,7 +478,7 @@ __device__ __forceinline__ float unpublish(uint32_t w) { return __uint_as_float(
 // hs * kWaves .. + kWaves - 1 serve KV head kvh_base + hs over the same
 // tiles, so with kH = 2 both halves of every slot row are requested by one
 // workgroup at the same time.
-template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH>
+template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH, bool kRope>
 __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkItem &it,
                                             int kvh_base) {
   constexpr int QK = D / 32;
@@ -553,7 +553,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // tile loads are in flight. The frequency is loaded here, before the tile
   // loads: memory loads complete in order, so a load issued after them
   // could only be used once they had all landed.
-  const bool rope = kAppend && p.inv_freq != nullptr;  // uniform
+  static_assert(kAppend || !kRope, "the rotary embedding rides on the fused write");
+  constexpr bool rope = kRope;
   __shared__ float rope_s[kWaves * kH][D];  // cos at [i], sin at [d/2 + i]
   float rope_freq = 0.f;
   if (rope && lane < D / 2) rope_freq = p.inv_freq[lane];
@@ -1034,13 +1035,13 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 // (sequence, split) are adjacent workgroups; the grid is sized for the widest
 // table and the workgroups past the live items exit after the context
 // lengths.
-template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH>
+template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH, bool kRope>
 __global__ __launch_bounds__(64 * kWaves * kH) void decode_mfma(DecodeParams p) {
   const int64_t cap = p.max_blocks * p.block_size;
   const int nhg = p.hkv / kH;  // KV-head groups per item
   const WorkItem it = find_item(p, blockIdx.x / nhg, cap);
   if (it.b < 0) return;  // uniform
-  decode_item<D, kBatch, kDouble, kAppend, kLds, kH>(p, it, (blockIdx.x % nhg) * kH);
+  decode_item<D, kBatch, kDouble, kAppend, kLds, kH, kRope>(p, it, (blockIdx.x % nhg) * kH);
 }
 
 }  // namespace
@@ -1051,16 +1052,26 @@ bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
          group >= 1 && group <= 16 && block_size % 16 == 0;
 }
 
-template <int D, int B, bool DB, bool A, bool L, int H = 1>
+template <int D, int B, bool DB, bool A, bool L, int H, bool R>
 int launch_one(const DecodeParams &p, hipStream_t stream) {
   // Every (sequence, split) item that can exist, times the KV-head groups.
   const int64_t items = (int64_t)p.batch * p.max_splits * (p.hkv / H);
   if (items > 0x7fffffff)
     return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_decode: %lld work items exceed the grid",
                      (long long)items);
-  decode_mfma<D, B, DB, A, L, H><<<dim3(static_cast<unsigned>(items)), 64 * kWaves * H, 0,
-                                   stream>>>(p);
+  decode_mfma<D, B, DB, A, L, H, R><<<dim3(static_cast<unsigned>(items)), 64 * kWaves * H, 0,
+                                      stream>>>(p);
   return check_launch("mlr_paged_decode(mfma)");
+}
+
+// The three variants of one layout: decode only, with the fused KV write,
+// and with the fused write and rotary embedding (their own instantiations,
+// so the rotary code costs the other two nothing).
+template <int D, int B, bool DB, bool L, int H = 1>
+int launch_variant(const DecodeParams &p, hipStream_t stream) {
+  if (p.new_k == nullptr) return launch_one<D, B, DB, false, L, H, false>(p, stream);
+  if (p.inv_freq == nullptr) return launch_one<D, B, DB, true, L, H, false>(p, stream);
+  return launch_one<D, B, DB, true, L, H, true>(p, stream);
 }
 
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
@@ -1068,7 +1079,6 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
   // needs no second register buffer (fewer VGPRs, more waves per SIMD); at
   // head_dim 64 a 320-token split lands its fifth tile per wave in LDS.
   const int tiles_per_wave = static_cast<int>(ceil_div(ceil_div(p.ts, 16), kWaves));
-  const bool append = p.new_k != nullptr;
   // Both KV heads of a pair go to one eight-wave workgroup when their GQA
   // groups fit the merge's 16 query-head rows and the paired grid still has a
   // workgroup for every CU. Measured: batch 64 x 14/2 heads, head_dim 64,
@@ -1079,33 +1089,22 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
   const int cus = current_device_cus();
   const bool pairs = p.hkv % 2 == 0 && 2 * p.group <= 16 && cus > 0 &&
                      (int64_t)p.batch * p.max_splits * (p.hkv / 2) >= cus;
-  // Instantiations: head_dim x (one load batch | + LDS tile | double-buffered) x append.
+  // Instantiations: head_dim x (one load batch | + LDS tile | double-buffered)
+  // x KV heads per workgroup x variant.
   if (p.d == 64) {
-    if (tiles_per_wave <= 4)
-      return append ? launch_one<64, 4, false, true, false>(p, stream)
-                    : launch_one<64, 4, false, false, false>(p, stream);
+    if (tiles_per_wave <= 4) return launch_variant<64, 4, false, false>(p, stream);
     if (p.ts == kLdsSplit64) {
-      if (pairs)
-        return append ? launch_one<64, 4, false, true, true, 2>(p, stream)
-                      : launch_one<64, 4, false, false, true, 2>(p, stream);
-      return append ? launch_one<64, 4, false, true, true>(p, stream)
-                    : launch_one<64, 4, false, false, true>(p, stream);
+      if (pairs) return launch_variant<64, 4, false, true, 2>(p, stream);
+      return launch_variant<64, 4, false, true>(p, stream);
     }
-    return append ? launch_one<64, 4, true, true, false>(p, stream)
-                  : launch_one<64, 4, true, false, false>(p, stream);
+    return launch_variant<64, 4, true, false>(p, stream);
   }
   if (pairs) {
-    if (tiles_per_wave <= 2)
-      return append ? launch_one<128, 2, false, true, false, 2>(p, stream)
-                    : launch_one<128, 2, false, false, false, 2>(p, stream);
-    return append ? launch_one<128, 2, true, true, false, 2>(p, stream)
-                  : launch_one<128, 2, true, false, false, 2>(p, stream);
+    if (tiles_per_wave <= 2) return launch_variant<128, 2, false, false, 2>(p, stream);
+    return launch_variant<128, 2, true, false, 2>(p, stream);
   }
-  if (tiles_per_wave <= 2)
-    return append ? launch_one<128, 2, false, true, false>(p, stream)
-                  : launch_one<128, 2, false, false, false>(p, stream);
-  return append ? launch_one<128, 2, true, true, false>(p, stream)
-                : launch_one<128, 2, true, false, false>(p, stream);
+  if (tiles_per_wave <= 2) return launch_variant<128, 2, false, false>(p, stream);
+  return launch_variant<128, 2, true, false>(p, stream);
 }
 
 }  // namespace mlr
