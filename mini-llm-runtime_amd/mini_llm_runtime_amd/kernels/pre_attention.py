@@ -154,8 +154,9 @@ def qkv_rope_decode(qkv: torch.Tensor, inv_freq: torch.Tensor, kv_cache: PagedKV
         raise ValueError(f"qkv must have shape [batch, {width}] with batch > 0, "
                          f"got {tuple(qkv.shape)}")
     batch = qkv.shape[0]
-    if qkv.stride(1) != 1 or qkv.stride(0) % 8 != 0:
-        qkv = qkv.contiguous()
+    if qkv.stride(1) != 1 or qkv.stride(0) % 8 != 0 or qkv.data_ptr() % 16 != 0:
+        # The kernel reads 16-byte aligned row chunks; a fresh copy is aligned.
+        qkv = qkv.clone(memory_format=torch.contiguous_format)
     if inv_freq.shape != (d // 2,):
         raise ValueError(f"inv_freq must have shape [{d // 2}]")
     for name, tensor in (("slot_mapping", slot_mapping), ("context_lens", context_lens)):

@@ -119,6 +119,26 @@ def test_bf16_inv_freq_and_strided_qkv_rows(device):
     assert torch.equal(got, want)
 
 
+def test_misaligned_qkv_rows_are_copied(device):
+    """Rows that start 2 bytes past a 16-byte boundary (a view one element
+    into a wider buffer) are copied to an aligned buffer first."""
+    hq, hkv, d, lens = 14, 2, 64, [77, 5]
+    qkv, kc, vc, bt, sl, slots, _ = _case(hq, hkv, d, lens, seed=5)
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
+    wide = torch.zeros(len(lens), qkv.shape[1] + 8, dtype=torch.bfloat16)
+    wide[:, 1:qkv.shape[1] + 1] = qkv
+    wide, bt, sl, slots = (t.to(device) for t in (wide, bt, sl, slots))
+    rows = wide[:, 1:qkv.shape[1] + 1]
+    assert rows.data_ptr() % 16 != 0
+
+    two_cache = _cache(kc, vc, device)
+    want, _ = _two_launches(rows.contiguous(), inv_freq, two_cache, bt, sl, slots, hq, 0)
+    one_cache = _cache(kc, vc, device)
+    got = kpre.qkv_rope_decode(rows, inv_freq, one_cache, 0, slots, bt, sl, hq)
+    assert torch.equal(one_cache.k_cache, two_cache.k_cache)
+    assert torch.equal(got, want)
+
+
 def test_repeated_steps_reuse_the_workspace(device):
     """Three decode steps in a row on one cache: each step's new row is read
     back by the next, and the shared workspace is left clean each time."""
