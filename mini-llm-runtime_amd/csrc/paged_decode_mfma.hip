@@ -89,18 +89,18 @@ __device__ __forceinline__ float bf16_elem(const uint4 &v, int e) {
 // Rotary embedding of one (x[i], x[i + d/2]) pair in bf16 as the reference's
 // apply_rotary_pos_emb computes it (model/qwen2.py:125-209), operation by
 // operation: each product and the sum rounded to bf16 (nearest even), no
-// fused multiply-add; the roundings go two at a time through
-// v_cvt_pk_bf16_f32.
+// fused multiply-add. The products are rounded here, two at a time through
+// v_cvt_pk_bf16_f32; the sums come back unrounded, and bf16_pack2 rounds
+// them as it packs two outputs into one word.
 __device__ __forceinline__ void rope_pair(float x_lo, float x_hi, float c, float s,
-                                          float &o_lo, float &o_hi) {
+                                          float &sum_lo, float &sum_hi) {
 #pragma clang fp contract(off)
   float a = x_lo * c, b = -x_hi * s;
   float e = x_hi * c, f = x_lo * s;
   bf16_round2(a, b);
   bf16_round2(e, f);
-  o_lo = a + b;
-  o_hi = e + f;
-  bf16_round2(o_lo, o_hi);
+  sum_lo = a + b;
+  sum_hi = e + f;
 }
 
 // Butterfly steps across lanes l ^ 16 and l ^ 32 as VALU lane swaps
