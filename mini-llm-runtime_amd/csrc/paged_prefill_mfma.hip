@@ -162,8 +162,25 @@ void prefill_mfma(PrefillParams p) {
   const int nitems = p.num_seqs * nqt;
   const int wr = workgroup_rank(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x),
                                 p.ncu, p.pair_cu);
-  const int rank = wr / p.hq;
-  const int h = wr % p.hq;
+  // Heads of one item on one XCD. The dispatcher deals workgroups to the 8
+  // XCDs in turn (blockIdx mod 8), and within each segment of
+  // workgroup_rank, wr mod 8 fixes blockIdx mod 8. For the ranks in whole
+  // groups of 8, wr = 8 (g hq + h) + x is rank 8g + x, head h: all heads of
+  // a rank share an XCD and its L2, so the K/V tiles of a GQA group come from
+  // HBM once rather than once per query head. Rank order (heaviest first)
+  // holds to within a group of 8. Ranks past the last whole group keep
+  // rank = wr / hq.
+  const int nranks = static_cast<int>(gridDim.x) / p.hq;
+  const int grouped = (nranks / 8) * 8 * p.hq;
+  int rank, h;
+  if (wr < grouped) {
+    const int t = wr >> 3;
+    rank = (t / p.hq) * 8 + (wr & 7);
+    h = t % p.hq;
+  } else {
+    rank = wr / p.hq;
+    h = wr % p.hq;
+  }
   int item;
   if (nitems <= kRankMax) {
     __shared__ int item_len[kRankMax];
