@@ -170,3 +170,38 @@ def test_shapes_outside_the_kernel_are_rejected(device):
     with pytest.raises(ValueError, match="head_dim 64 or 128"):
         kpre.qkv_rope_decode(qkv, torch.ones(16, device=device), cache, 0, one - 1,
                              torch.zeros(1, 1, dtype=torch.long, device=device), one, 4)
+
+
+def test_one_launch_step_in_graph_replays(device):
+    """The one-launch step captured in a HIP graph and replayed four times,
+    with new projection rows copied in eagerly between replays: every replay
+    equals an eager call on a copy of the cache, output and cache bits."""
+    hq, hkv, d = 14, 2, 64
+    lens = [33, 600, 1500, 4000, 257]
+    qkv, kc, vc, bt, sl, slots, _ = _case(hq, hkv, d, lens, seed=41)
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
+    qkv, bt, sl, slots = (t.to(device) for t in (qkv, bt, sl, slots))
+    cache = _cache(kc, vc, device)
+    out = torch.empty(len(lens), hq, d, dtype=torch.bfloat16, device=device)
+    ws = torch.zeros(kpa.decode_workspace_bytes(len(lens), hq, d, bt.shape[1] * BS,
+                                                torch.bfloat16),
+                     dtype=torch.uint8, device=device)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        kpre.qkv_rope_decode(qkv, inv_freq, cache, 0, slots, bt, sl, hq, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        kpre.qkv_rope_decode(qkv, inv_freq, cache, 0, slots, bt, sl, hq, out=out, workspace=ws)
+    gen = torch.Generator().manual_seed(4)
+    for _ in range(4):
+        qkv.copy_(torch.randn(qkv.shape, generator=gen).to(torch.bfloat16).to(device))
+        eager_cache = _cache(cache.k_cache[0].clone(), cache.v_cache[0].clone(), device)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = kpre.qkv_rope_decode(qkv, inv_freq, eager_cache, 0, slots, bt, sl, hq)
+        assert torch.equal(out, eager)
+        assert torch.equal(cache.k_cache, eager_cache.k_cache)
+        assert torch.equal(cache.v_cache, eager_cache.v_cache)
