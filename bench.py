@@ -277,6 +277,19 @@ def profile_run(args, device):
     print("profile: 3 copies of 1 GiB", flush=True)
 
 
+def check_decode_outputs(kpa, workspace, out, stream, what):
+    """A split merge that gave up waiting writes only NaN. After a timed
+    region, the workspace's merge-failure flag (mlr_paged_decode_workspace_check,
+    which raises DecodeMergeError) and the last outputs must be clean."""
+    import torch
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        kpa.check_workspace(workspace)
+    if not bool(torch.isfinite(out).all()):
+        raise RuntimeError(f"{what}: non-finite decode outputs after the timed region")
+
+
 def bench_decode(args, device):
     import torch
 
@@ -370,6 +383,8 @@ def bench_decode(args, device):
         warm_graph(g, stream)
         res[kind] = timed_graph(g, 10, stream) / (10 * LAYERS)
     sclk = sample_sclk(g_steps.replay)
+    g_steps.replay()  # the last graph to write `out` is the timed step's
+    check_decode_outputs(kpa, workspace, out, stream, wl.name)
     decode_bytes = wl.algorithmic_bytes()
     step_bytes = decode_bytes + wl.write_bytes()
     sec_per_step = t_step / steps
@@ -592,6 +607,7 @@ def bench_decode_32k(device, reps=4, calls_per_graph=6):
                 step(i)
         warm_graph(g, stream)
         us = timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
+        check_decode_outputs(kpa, ws, out, stream, f"{wl.name} ({splits} splits)")
         sweep["default" if splits == 0 else str(splits)] = round(us, 2)
     best = min(sweep, key=sweep.get)
     best_us = sweep[best]
@@ -734,6 +750,7 @@ def bench_fp32_decode_b4(device, budget):
             call()
     warm_graph(g, stream, seconds=0.1)
     gpu_us = timed_graph(g, 10, stream) / 100 * 1e6
+    check_decode_outputs(kpa, ws, out, stream, wl.name)
 
     threads = _cpu_threads()
     cache = OracleKVCache(1, wl.k_cache.shape[0], 16, 2, 64, dtype=torch.float32)

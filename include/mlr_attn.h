@@ -55,7 +55,9 @@ enum mlr_status {
   MLR_ERR_INVALID = 1,     /* bad argument (shape, stride, pointer, size)  */
   MLR_ERR_UNSUPPORTED = 2, /* valid, but outside what the kernels cover     */
   MLR_ERR_WORKSPACE = 3,   /* workspace missing or too small                */
-  MLR_ERR_HIP = 4          /* the HIP runtime reported an error at launch   */
+  MLR_ERR_HIP = 4,         /* the HIP runtime reported an error at launch   */
+  MLR_ERR_MERGE = 5        /* a decode workspace's merge-failure flag was set
+                              (see mlr_paged_decode_workspace_check)        */
 };
 
 /* Message describing the last failed call on this thread ("" if none). */
@@ -126,7 +128,8 @@ size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
  *                  overlap. Should a merge ever wait past its limit (it waits
  *                  only for workgroups launched before its own), it sets the
  *                  workspace's first word and writes NaN, and so does every
- *                  later merge on that workspace until it is zeroed again.
+ *                  later merge on that workspace until it is cleared:
+ *                  mlr_paged_decode_workspace_check reports and clears it.
  *   out          : [batch, num_q_heads, head_dim], strides (out_stride_b, out_stride_h)
  */
 int mlr_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -215,6 +218,8 @@ int mlr_paged_decode_qkv(
  *     GPU (other streams, other threads) race and must not be issued.
  *   - Arguments, results and cache contents are those of
  *     mlr_paged_decode_append with the same inputs (the same kernels run).
+ *   - A merge failure on the array (see mlr_paged_decode_workspace_check) is
+ *     reported and cleared by mlr_paged_decode_static_check, outside capture.
  */
 int mlr_paged_decode_append_static(
     const void *q, int64_t q_stride_b, int64_t q_stride_h, void *k_cache,
@@ -225,6 +230,30 @@ int mlr_paged_decode_append_static(
     const void *new_k, const void *new_v, int64_t new_stride_b,
     int64_t new_stride_h, const int64_t *slot_mapping, void *out,
     int64_t out_stride_b, int64_t out_stride_h, void *stream);
+
+/*
+ * Merge-failure check of a decode workspace, and its recovery. The bf16
+ * single-launch merge of mlr_paged_decode and its variants waits only for
+ * workgroups launched before its own, with a bounded wait; should that wait
+ * ever give up, the merge sets the workspace's flag word and writes NaN, and
+ * every later multi-split merge on the workspace writes NaN too (partial rows
+ * it left behind may be stale). This call waits for `stream`, reads the flag
+ * word and returns MLR_OK when it is clear. When it is set, it zeroes the
+ * whole workspace (a fill kernel on `stream`, then a wait) and returns
+ * MLR_ERR_MERGE: the outputs of the multi-split decodes since the failure
+ * are NaN and must be recomputed; the workspace is usable again. It
+ * synchronises the host, so it is refused (MLR_ERR_INVALID) while `stream`
+ * is being captured into a graph; no other stream may be using the
+ * workspace meanwhile.
+ *
+ * No counterpart in the reference, whose PyTorch decode cannot fail this way;
+ * it keeps the reference's contract that failures surface as errors
+ * (runtime/paged_kv_cache.py:228-239) rather than as silent values.
+ * mlr_paged_decode_static_check does the same for the library's own scratch of
+ * mlr_paged_decode_append_static on the current device.
+ */
+int mlr_paged_decode_workspace_check(void *workspace, size_t workspace_bytes, void *stream);
+int mlr_paged_decode_static_check(void *stream);
 
 /*
  * Paged chunk-prefill attention for a packed batch of sequences (varlen):

@@ -17,6 +17,7 @@
 // bf16 inputs with head_dim 64 or 128 and at most 16 query heads per KV head
 // take the MFMA kernel in paged_decode_mfma.hip; everything else takes the
 // generic kernel below.
+#include <algorithm>
 #include <atomic>
 
 #include "mlr_common.h"
@@ -605,4 +606,73 @@ extern "C" int mlr_paged_decode_append_static(
                      "with a workspace instead", kStaticScratchBytes, why);
   }
   return rc;
+}
+
+// ---------------------------------------------------------------------------
+// Merge-failure check and recovery of a decode workspace (or of the static
+// scratch): read the flag word; when it is set, zero the whole workspace.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Zeroes `bytes` bytes at p (16-byte aligned): 16-byte stores, then the tail.
+__global__ __launch_bounds__(256) void zero_bytes(unsigned char *p, size_t bytes) {
+  const size_t n16 = bytes / 16;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+    reinterpret_cast<uint4 *>(p)[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (blockIdx.x == 0 && threadIdx.x < bytes % 16) p[16 * n16 + threadIdx.x] = 0;
+}
+
+int check_and_clear(void *ws, size_t bytes, hipStream_t s, const char *what) {
+  MLR_REQUIRE(ws != nullptr && bytes >= static_cast<size_t>(kFlagBytes),
+              "%s: the workspace must hold at least its %lld-byte flag region", what,
+              (long long)kFlagBytes);
+  MLR_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 255u) == 0,
+              "%s: workspace must be 256-byte aligned", what);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t err = hipStreamIsCapturing(s, &cap);
+  if (err != hipSuccess)
+    return set_error(MLR_ERR_HIP, "%s: hipStreamIsCapturing failed: %s", what,
+                     hipGetErrorString(err));
+  MLR_REQUIRE(cap == hipStreamCaptureStatusNone,
+              "%s: the stream is being captured; the check synchronises and must run "
+              "outside capture", what);
+  uint32_t flag = 0;
+  err = hipMemcpyAsync(&flag, ws, sizeof(flag), hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  if (err != hipSuccess)
+    return set_error(MLR_ERR_HIP, "%s: reading the flag word failed: %s", what,
+                     hipGetErrorString(err));
+  if (flag == 0u) return MLR_OK;
+  const size_t blocks = std::min<size_t>(1024, (bytes / 16 + 255) / 256 + 1);
+  zero_bytes<<<dim3(static_cast<unsigned>(blocks)), 256, 0, s>>>(static_cast<unsigned char *>(ws),
+                                                                   bytes);
+  int rc = check_launch(what);
+  if (rc != MLR_OK) return rc;
+  err = hipStreamSynchronize(s);
+  if (err != hipSuccess)
+    return set_error(MLR_ERR_HIP, "%s: clearing the workspace failed: %s", what,
+                     hipGetErrorString(err));
+  return set_error(MLR_ERR_MERGE,
+                   "%s: a single-launch split merge gave up waiting for its partial results; "
+                   "the multi-split decode outputs computed on this workspace since then are "
+                   "NaN. The workspace has been cleared and can be used again.", what);
+}
+
+}  // namespace
+
+extern "C" int mlr_paged_decode_workspace_check(void *workspace, size_t workspace_bytes,
+                                                void *stream) {
+  clear_error();
+  return check_and_clear(workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                         "mlr_paged_decode_workspace_check");
+}
+
+extern "C" int mlr_paged_decode_static_check(void *stream) {
+  clear_error();
+  void *ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != MLR_OK) return rc;
+  return check_and_clear(ws, kStaticScratchBytes, static_cast<hipStream_t>(stream),
+                         "mlr_paged_decode_static_check");
 }

@@ -568,7 +568,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // Rotates the lane's q fragments: fragment j < QK/2 holds dims
   // 32j + 8g + e (e < 8) and fragment j + QK/2 their partners d/2 further, so
   // each pair is in one lane. LDS operations of one wave complete in order,
-  // so the wave reads back the cos/sin it has just written.
+  // so the wave reads back the cos/sin it has just written; the wave barrier
+  // (no instruction) keeps the compiler from moving the other lanes' reads
+  // above those writes.
   auto rotate_q = [&]() {
     if (lane < D / 2) {
       // sincosf shares one argument reduction between the two; its results
@@ -579,6 +581,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       rope_s[wave][lane] = cs;
       rope_s[wave][D / 2 + lane] = sn;
     }
+    __builtin_amdgcn_wave_barrier();
     if (!head_ok) return;  // columns past the group stay zero
 #pragma unroll
     for (int j = 0; j < QK / 2; ++j) {
@@ -669,6 +672,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         *reinterpret_cast<uint4 *>(dst) = v;
       }
     }
+    // Every lane of this wave reads the staged rows at compute time.
+    __builtin_amdgcn_wave_barrier();
   };
   // Marks row last_tok of the new token's tile for substitution when the
   // new slot is the one position ctx - 1 maps to.

@@ -74,6 +74,8 @@ _PROTOTYPES = {
          _c_int, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr,
          _c_i64, _c_i64, _c_ptr],
     ),
+    "mlr_paged_decode_workspace_check": (_c_int, [_c_ptr, _c_size, _c_ptr]),
+    "mlr_paged_decode_static_check": (_c_int, [_c_ptr]),
     "mlr_paged_prefill": (
         _c_int,
         [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64,
@@ -115,6 +117,10 @@ class NativeLibraryError(RuntimeError):
 
 class KernelError(RuntimeError):
     """A C-ABI entry point returned a non-zero status."""
+
+
+# enum mlr_status in include/mlr_attn.h
+MLR_ERR_MERGE = 5
 
 
 _lock = threading.Lock()

@@ -57,20 +57,77 @@ def _require_kernel_layout(q: torch.Tensor, k_cache: torch.Tensor,
 # decode kernels exchange split partials through the workspace, a zero word
 # meaning "not written yet"; it must be zero when a call starts, and every
 # call leaves it zero. One workspace per stream keeps calls on different
-# streams from sharing partials.
+# streams from sharing partials. A workspace that a larger one replaces stays
+# allocated (in _RETIRED) for the life of the process: a graph captured
+# earlier may still replay on its address.
 _WORKSPACES: dict = {}
+_RETIRED: list = []
+
+
+class DecodeMergeError(RuntimeError):
+    """A decode workspace's merge-failure flag was set: the multi-split
+    decode outputs computed on it since the failure are NaN. The workspace
+    has been cleared and is usable again."""
 
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A zero-initialised decode workspace of at least `nbytes` for the
-    current stream of `device`, reused across calls."""
+    current stream of `device`, reused across calls.
+
+    Under graph capture the cached workspace is used as it is: allocating or
+    growing one there would only record its zero fill into the graph (the
+    memory would hold garbage until the first replay), so that case raises
+    and asks for an eager call of the same size first, or an explicit
+    workspace.
+    """
     stream = torch.cuda.current_stream(device).cuda_stream
     key = (device.index, stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            have = 0 if ws is None else ws.numel()
+            raise RuntimeError(
+                f"paged decode under graph capture needs a {nbytes}-byte decode workspace "
+                f"for this stream and the cached one has {have} bytes; run one eager call "
+                "of the same size on this stream before capturing, or pass workspace=")
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+def check_workspace(workspace: torch.Tensor) -> None:
+    """Raise DecodeMergeError when `workspace`'s merge-failure flag is set
+    (after clearing the workspace); synchronises torch's current stream and
+    must run outside graph capture (mlr_paged_decode_workspace_check)."""
+    lib = _lib.load()
+    device = workspace.device
+    with torch.cuda.device(device):
+        status = lib.mlr_paged_decode_workspace_check(
+            workspace.data_ptr(), workspace.numel(), _lib.stream_handle(device))
+    if status == _lib.MLR_ERR_MERGE:
+        raise DecodeMergeError(lib.mlr_last_error().decode(errors="replace"))
+    _lib.check(status, "mlr_paged_decode_workspace_check")
+
+
+def check_decode_workspaces(device: torch.device | None = None) -> None:
+    """Check every cached decode workspace (of `device`, or of all devices)
+    for a merge failure, once the work queued on them has finished; raises
+    DecodeMergeError if any flag was set, after clearing every flagged
+    workspace. The model runner calls this once per step."""
+    failures = []
+    cached = [ws for (index, _stream), ws in list(_WORKSPACES.items())
+              if device is None or index == device.index]
+    for dev in {ws.device for ws in cached}:
+        torch.cuda.synchronize(dev)  # the workspaces' own streams included
+    for ws in cached:
+        try:
+            check_workspace(ws)
+        except DecodeMergeError as exc:
+            failures.append(str(exc))
+    if failures:
+        raise DecodeMergeError("; ".join(failures))
 
 
 def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int,

@@ -14,6 +14,10 @@ decode forward, as in the reference. Logits come back in packed token order
 whatever the order of phases in the batch. The batch checks are the
 reference's, with its messages and order, evaluated with two host syncs
 instead of several per request.
+
+``run_generation_step`` also checks the decode workspaces once per step: a
+split merge that gave up waiting (it only writes NaN) raises
+``DecodeMergeError`` there instead of reaching the sampled tokens unnoticed.
 """
 
 from __future__ import annotations
@@ -22,6 +26,7 @@ from dataclasses import dataclass
 
 import torch
 
+from ..kernels import paged_attention as kpa
 from .paged_kv_cache import PagedKVCache
 from .request import Request, RequestStatus
 from .scheduler import Scheduler, SchedulerOutput
@@ -341,6 +346,9 @@ def run_generation_step(model, scheduler: Scheduler,
                               device=scheduler.kv_cache.device)
     packed_logits = execute_model_batch(model=model, batch=batch, kv_cache=scheduler.kv_cache)
     sampled = greedy_sample(packed_logits, batch)
+    if batch.input_token_ids.device.type == "cuda":
+        # Before any sampled token is committed to the scheduler.
+        kpa.check_decode_workspaces(batch.input_token_ids.device)
     eos = ({rid for rid, tok in sampled.items() if tok == eos_token_id}
            if eos_token_id is not None else set())
     finished = scheduler.update_after_model(scheduler_output=scheduler_output,

@@ -251,6 +251,42 @@ def test_qwen05b_b64_decode_with_write(device):
     assert err <= 2e-2
 
 
+def test_qwen05b_b64_append_step_matches_oracle(device):
+    """The timed decode step at full size (batch 64, contexts U[128, 4096]):
+    paged_decode_launch with new_k/new_v/slot_mapping, i.e.
+    mlr_paged_decode_append, the 64-token KV write folded into the split
+    decode. Its cache equals the oracle's write_slots bit for bit, its output
+    is within 2e-2 of the oracle's write_slots + decode_batch_parallel on
+    every (sequence, head) row, and it equals mlr_kv_write followed by
+    mlr_paged_decode on the GPU bit for bit."""
+    wl = workloads.bf16_decode_qwen05b_b64()
+    kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
+    kc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.new_k)
+    vc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.new_v)
+    want = opa.decode_batch_parallel(wl.q, kc, vc, wl.block_tables, wl.context_lens, 16)
+    q, bt, sl = wl.q.to(device), wl.block_tables.to(device), wl.context_lens.to(device)
+    slots = wl.slot_mapping.to(device)
+
+    fused = PagedKVCache(1, kc.shape[0], 16, 2, 64, dtype=torch.bfloat16, device=device)
+    fused.k_cache[0].copy_(wl.k_cache)
+    fused.v_cache[0].copy_(wl.v_cache)
+    k_layer, v_layer = fused.get_layer_cache(0)
+    got = kpa.paged_decode_launch(q, k_layer, v_layer, bt, sl, new_k=wl.new_k.to(device),
+                                  new_v=wl.new_v.to(device), slot_mapping=slots)
+    assert torch.equal(k_layer.cpu(), kc) and torch.equal(v_layer.cpu(), vc)
+    err = max_abs(got, want)
+    print(f"qwen05b_b64 append step max-abs vs oracle: {err:.3e}")
+    assert torch.isfinite(got).all()
+    assert err <= 2e-2
+
+    pair = PagedKVCache(1, kc.shape[0], 16, 2, 64, dtype=torch.bfloat16, device=device)
+    pair.k_cache[0].copy_(wl.k_cache)
+    pair.v_cache[0].copy_(wl.v_cache)
+    pair.write_slots(slots, wl.new_k.to(device), wl.new_v.to(device))
+    k2, v2 = pair.get_layer_cache(0)
+    assert torch.equal(got, kpa.paged_decode_launch(q, k2, v2, bt, sl))
+
+
 def _textbook_row(q_row, kc, vc, table, length, kv_head, bs):
     """float64 attention of one query row over one sequence (vectorised)."""
     pos = torch.arange(length)
@@ -454,3 +490,122 @@ def test_merge_distrusts_a_flagged_workspace(device):
             assert max_abs(got[i], want[i]) <= 2e-2, i
         else:
             assert torch.isnan(got[i]).all(), i
+
+
+def _flag_case(device):
+    lens = [100, 1000, 3000, 320, 321, 17]
+    q, kc, vc, bt, sl, tables = random_paged(lens, 14, 2, 64, 16, dtype=torch.bfloat16, seed=5)
+    want = opa.decode_batch_loop(q, kc, vc, tables, lens, 16)
+    args = tuple(t.to(device) for t in (q, kc, vc, bt, sl))
+    return lens, args, want
+
+
+def test_flagged_workspace_is_reported_and_cleared(device):
+    """mlr_paged_decode_workspace_check on a workspace whose merge-failure
+    flag is set (from the host, as a merge that waited past its limit would
+    leave it; every kernel exits normally): it raises DecodeMergeError, the
+    whole workspace is zero afterwards (the flag and the partial rows the
+    distrusting merges left behind), and the next decode on it is exact.
+    A clean workspace passes."""
+    lens, args, want = _flag_case(device)
+    ts = 320
+    ws = torch.zeros(kpa.decode_workspace_bytes(len(lens), 14, 64, args[3].shape[1] * 16,
+                                                torch.bfloat16, ts),
+                     dtype=torch.uint8, device=device)
+    kpa.check_workspace(ws)  # clean: no error
+    ws[:4].view(torch.int32).fill_(1)
+    got = kpa.paged_decode_launch(*args, tokens_per_split=ts, workspace=ws)
+    assert torch.isnan(got[1]).all()
+    assert int(torch.count_nonzero(ws[256:])) > 0  # partials of distrusted merges
+    with pytest.raises(kpa.DecodeMergeError, match="gave up waiting"):
+        kpa.check_workspace(ws)
+    assert int(torch.count_nonzero(ws)) == 0
+    kpa.check_workspace(ws)
+    got = kpa.paged_decode_launch(*args, tokens_per_split=ts, workspace=ws)
+    assert max_abs(got, want) <= 2e-2
+    assert int(torch.count_nonzero(ws)) == 0
+
+
+def test_cached_workspace_flag_raises_in_the_step_check(device):
+    """The per-stream workspace the Python layer keeps: a set flag makes
+    check_decode_workspaces (called by run_generation_step once per step)
+    raise DecodeMergeError; the workspace is cleared and later calls are
+    exact. The test runs on a stream of its own, so its cached workspace is
+    the one it flags."""
+    lens, args, want = _flag_case(device)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        kpa.paged_decode_launch(*args, tokens_per_split=320)
+        ws = kpa.decode_workspace(device, 256)  # this stream's cached workspace
+        ws[:4].view(torch.int32).fill_(1)
+        got = kpa.paged_decode_launch(*args, tokens_per_split=320)
+        assert torch.isnan(got[1]).all()
+        with pytest.raises(kpa.DecodeMergeError):
+            kpa.check_decode_workspaces(device)
+        assert int(torch.count_nonzero(ws)) == 0
+        kpa.check_decode_workspaces(device)
+        got = kpa.paged_decode_launch(*args, tokens_per_split=320)
+        assert max_abs(got, want) <= 2e-2
+    torch.cuda.synchronize()
+
+
+def test_workspace_check_is_refused_under_capture(device):
+    """The check synchronises the host, so it refuses a stream under graph
+    capture (before touching the stream) instead of breaking the capture."""
+    ws = torch.zeros(4096, dtype=torch.uint8, device=device)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        with pytest.raises(RuntimeError, match="captured"):
+            kpa.check_workspace(ws)
+        ws.add_(0)  # keeps the graph non-empty
+    torch.cuda.synchronize()
+
+
+def test_cached_workspace_under_graph_capture(device):
+    """Decode without workspace= inside graph capture. A cached workspace that
+    is too small is not replaced inside the capture (that would record only
+    its zero fill, leaving it uninitialised until a replay): the call raises
+    and asks for an eager call first. After an eager call of the captured
+    size on the same stream, capture uses the cached workspace, and every
+    replay (new queries copied in eagerly between replays) equals an eager
+    call bit for bit. A workspace that a larger one replaced stays allocated
+    (graphs captured on it keep a live address)."""
+    small = [40, 700]
+    big = [33, 600, 1500, 4000, 257]
+    qs, kcs, vcs, bts, sls, _ = random_paged(small, 14, 2, 64, 16, dtype=torch.bfloat16, seed=76)
+    q, kc, vc, bt, sl, _ = random_paged(big, 14, 2, 64, 16, dtype=torch.bfloat16, seed=77)
+    qs, kcs, vcs, bts, sls = (t.to(device) for t in (qs, kcs, vcs, bts, sls))
+    q, kc, vc, bt, sl = (t.to(device) for t in (q, kc, vc, bt, sl))
+    out = torch.empty_like(q)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        kpa.paged_decode_launch(qs, kcs, vcs, bts, sls)  # caches a small workspace
+        small_ws = kpa.decode_workspace(device, 256)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        with pytest.raises(RuntimeError, match="eager call"):
+            kpa.paged_decode_launch(q, kc, vc, bt, sl, out)
+        out.add_(0)  # keeps the graph non-empty
+    with torch.cuda.stream(stream):
+        kpa.paged_decode_launch(q, kc, vc, bt, sl, out)  # grows the cached workspace
+        grown = kpa.decode_workspace(device, 256)
+    torch.cuda.synchronize()
+    assert grown.numel() > small_ws.numel()
+    assert any(r is small_ws for r in kpa._RETIRED)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        kpa.paged_decode_launch(q, kc, vc, bt, sl, out)
+    gen = torch.Generator().manual_seed(4)
+    for _ in range(4):
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(device))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = kpa.paged_decode_launch(q, kc, vc, bt, sl)
+        assert torch.equal(replayed, eager)

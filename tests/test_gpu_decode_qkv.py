@@ -205,3 +205,56 @@ def test_one_launch_step_in_graph_replays(device):
         assert torch.equal(out, eager)
         assert torch.equal(cache.k_cache, eager_cache.k_cache)
         assert torch.equal(cache.v_cache, eager_cache.v_cache)
+
+
+def test_qwen05b_b64_served_step_matches_oracle(device):
+    """The served decode step (what forward_decode_batch_with_cache runs after
+    its QKV GEMM) at full size: batch 64, 14/2 heads, head_dim 64, contexts
+    U[128, 4096] in a 24,576-block pool. qkv_rope_decode against the oracle's
+    rotary embedding (rope_tables + rotate at position ctx - 1, the
+    reference's model/qwen2.py:125-209 restated), write_slots and
+    decode_batch_parallel: output within 2e-2 on every (sequence, head) row,
+    written V rows bit-exact, written K rows within two bf16 ulps of the
+    terms of the oracle's (cos/sin come from the device's and the host's
+    libraries); and
+    equal bit for bit to mlr_qkv_rope_write followed by the decode."""
+    import oracle.qwen2_attention as oqa
+    from mini_llm_runtime_amd import workloads
+
+    wl = workloads.bf16_decode_qwen05b_b64()
+    hq, hkv, d = 14, 2, 64
+    gen = torch.Generator().manual_seed(64)
+    qkv = torch.randn(64, (hq + 2 * hkv) * d, generator=gen).bfloat16()
+    q = qkv[:, :hq * d].reshape(64, hq, d)
+    k_new = qkv[:, hq * d:(hq + hkv) * d].reshape(64, hkv, d)
+    v_new = qkv[:, (hq + hkv) * d:].reshape(64, hkv, d)
+    cos, sin = oqa.rope_tables(wl.context_lens - 1, d, THETA, torch.bfloat16)
+    q_rot, k_rot = oqa.rotate(q, cos, sin), oqa.rotate(k_new, cos, sin)
+    kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
+    kc.view(-1, hkv, d).index_copy_(0, wl.slot_mapping, k_rot)
+    vc.view(-1, hkv, d).index_copy_(0, wl.slot_mapping, v_new)
+    want = opa.decode_batch_parallel(q_rot, kc, vc, wl.block_tables, wl.context_lens, BS)
+
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
+    qkv_d, bt, sl, slots = (t.to(device) for t in (qkv, wl.block_tables, wl.context_lens,
+                                                      wl.slot_mapping))
+    one_cache = _cache(wl.k_cache, wl.v_cache, device)
+    got = kpre.qkv_rope_decode(qkv_d, inv_freq, one_cache, 0, slots, bt, sl, hq)
+    err = (got.double().cpu() - want.double()).abs().max().item()
+    print(f"qwen05b_b64 served step max-abs vs oracle: {err:.3e}")
+    assert torch.isfinite(got).all()
+    assert err <= 2e-2
+    k_rows = one_cache.k_cache[0].view(-1, hkv, d).index_select(0, slots).cpu()
+    v_rows = one_cache.v_cache[0].view(-1, hkv, d).index_select(0, slots).cpu()
+    assert torch.equal(v_rows, v_new)
+    # A one-ulp change of cos or sin moves each product by at most one ulp
+    # of that product: two bf16 ulps (2^-7 relative) of the terms
+    # |x_lo| + |x_hi|, not of their possibly cancelling sum.
+    x = k_new.double()
+    mag = x.abs() + torch.cat((x[..., d // 2:], x[..., :d // 2]), dim=-1).abs()
+    assert ((k_rows.double() - k_rot.double()).abs() <= 2 * 2.0 ** -7 * mag).all()
+
+    two_cache = _cache(wl.k_cache, wl.v_cache, device)
+    pair, _ = _two_launches(qkv_d, inv_freq, two_cache, bt, sl, slots, hq, 0)
+    assert torch.equal(one_cache.k_cache, two_cache.k_cache)
+    assert torch.equal(got, pair)

@@ -5,7 +5,10 @@ with a caller workspace, through the C ABI.
 The two entry points run the same kernels, so outputs and the K/V written to
 the cache must be identical bit for bit. Two calls in a row, the second with a
 smaller batch (the scratch keeps the first call's contents), then an oversized
-request that must be rejected before anything is launched or written.
+request that must be rejected before anything is launched or written. The
+call is also captured into a graph (where allocation is refused) and its
+replays compared with the workspace entry point, and the scratch's
+merge-failure check (mlr_paged_decode_static_check) runs on the clean scratch.
 """
 
 from __future__ import annotations
@@ -103,3 +106,64 @@ def test_static_scratch_rejects_oversized_requests_before_writing(device):
     assert "mlr_paged_decode_append_static" in msg and "8388608" in msg
     assert torch.equal(kc, before_k)
     assert torch.all(out == 7.0)
+
+
+def test_static_scratch_decode_under_graph_capture(device):
+    """The property the entry point exists for: it runs inside graph capture
+    (torch's capture refuses device allocation from any thread) and every
+    replay, with new queries copied in eagerly between replays, equals the
+    workspace entry point's result bit for bit. One eager warm-up first
+    (it loads the code object and looks up the scratch address)."""
+    lens = [33, 600, 1500, 4000, 257, 1]
+    q, kc, vc, bt, sl, tables = random_paged(lens, 14, 2, 64, 16, dtype=torch.bfloat16,
+                                             seed=21, fill=0.0)
+    gen = torch.Generator().manual_seed(22)
+    new_k = torch.randn(len(lens), 2, 64, generator=gen).bfloat16()
+    new_v = torch.randn(len(lens), 2, 64, generator=gen).bfloat16()
+    slots = torch.tensor([tables[b][(n - 1) // 16] * 16 + (n - 1) % 16
+                          for b, n in enumerate(lens)])
+    q, kc, vc, bt, sl, new_k, new_v, slots = (t.to(device) for t in
+                                              (q, kc, vc, bt, sl, new_k, new_v, slots))
+    k2, v2 = kc.clone(), vc.clone()
+    out = torch.empty_like(q)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        assert _static_call(q, kc, vc, bt, sl, new_k, new_v, slots, out) == 0
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        rc = _static_call(q, kc, vc, bt, sl, new_k, new_v, slots, out)
+    assert rc == 0, _lib.load().mlr_last_error()
+    ws = torch.zeros(kpa.decode_workspace_bytes(len(lens), 14, 64, bt.shape[1] * 16,
+                                                torch.bfloat16),
+                     dtype=torch.uint8, device=device)
+    for _ in range(4):
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(device))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        want = kpa.paged_decode_launch(q, k2, v2, bt, sl, workspace=ws, new_k=new_k,
+                                       new_v=new_v, slot_mapping=slots)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, want)
+        assert torch.equal(kc, k2) and torch.equal(vc, v2)
+
+
+def test_static_scratch_check(device):
+    """mlr_paged_decode_static_check: MLR_OK on the clean scratch after the
+    calls above (every call leaves it zero), and refused under capture."""
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        assert lib.mlr_paged_decode_static_check(_lib.stream_handle(device)) == 0, \
+            lib.mlr_last_error()
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    x = torch.zeros(4, device=device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        rc = lib.mlr_paged_decode_static_check(_lib.stream_handle(device))
+        x.add_(1)  # keeps the graph non-empty
+    assert rc == 1  # MLR_ERR_INVALID
+    assert "captured" in lib.mlr_last_error().decode()
