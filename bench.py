@@ -328,6 +328,22 @@ def bench_decode(args, device):
     floor_items = (64, 96, 160, 320)
     floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // min(floor_items)), dtype=torch.int32,
                             device=device)
+    # Contiguous comparators (the reference times dense attention on
+    # contiguous K/V beside its paged decode): the same context lengths with
+    # each sequence's blocks consecutive in the pool (bt_seq), and the same
+    # token rows as one run of consecutive blocks (bt_flat, one sequence).
+    need = [-(-int(n) // 16) for n in wl.context_lens.tolist()]
+    starts = [sum(need[:b]) for b in range(64)]
+    bt_seq = torch.full_like(wl.block_tables, -1)
+    for b, (s0, n) in enumerate(zip(starts, need)):
+        bt_seq[b, :n] = torch.arange(s0, s0 + n)
+    slots_seq = torch.tensor([int(bt_seq[b, (n - 1) // 16]) * 16 + (n - 1) % 16
+                              for b, n in enumerate(wl.context_lens.tolist())])
+    total_tokens = int(wl.context_lens.sum())
+    bt_flat = torch.arange(-(-total_tokens // 16)).unsqueeze(0)
+    bt_seq, slots_seq, bt_flat = (t.to(device) for t in (bt_seq, slots_seq, bt_flat))
+    ctx_flat = torch.tensor([total_tokens], device=device)
+    flat_out = torch.empty(-(-bt_flat.shape[1] * 16 // 96), dtype=torch.int32, device=device)
 
     def step(layer, kind="step"):
         k_layer, v_layer = cache.get_layer_cache(layer)
@@ -338,6 +354,16 @@ def bench_decode(args, device):
         elif kind == "decode":  # decode only
             kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out,
                                     tokens_per_split=ts, workspace=workspace)
+        elif kind == "contig":  # the step on per-sequence contiguous blocks
+            kpa.paged_decode_launch(q, k_layer, v_layer, bt_seq, ctx, out, tokens_per_split=ts,
+                                    workspace=workspace, new_k=new_k, new_v=new_v,
+                                    slot_mapping=slots_seq)
+        elif kind == "floor_seq":  # read floor on per-sequence contiguous blocks
+            kpa.paged_kv_read_floor(k_layer, v_layer, bt_seq, ctx, tokens_per_item=96,
+                                    out=floor_out)
+        elif kind == "floor_flat":  # the same rows as one contiguous run
+            kpa.paged_kv_read_floor(k_layer, v_layer, bt_flat, ctx_flat, tokens_per_item=96,
+                                    out=flat_out)
         elif kind.startswith("floor"):  # read-only pass over the same K/V rows
             kpa.paged_kv_read_floor(k_layer, v_layer, bt, ctx,
                                     tokens_per_item=int(kind[5:]), out=floor_out)
@@ -376,7 +402,7 @@ def bench_decode(args, device):
     # A larger sample of the same graph (10 replays) as a cross-check.
     t_step10 = timed_graph(g_steps, 10, stream) / 10
     graphs = {kind: capture(kind, LAYERS)
-              for kind in ("decode", "served", "served1",
+              for kind in ("decode", "served", "served1", "contig", "floor_seq", "floor_flat",
                            *(f"floor{n}" for n in floor_items))}
     res = {}
     for kind, g in graphs.items():
@@ -402,6 +428,18 @@ def bench_decode(args, device):
         "GBps": round(kv_bytes / (floor_us[best] * 1e-6) / 1e9, 1),
         "frac_of_hbm_peak": round(kv_bytes / (floor_us[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "step_us_over_floor_us": round(sec_per_step * 1e6 / floor_us[best], 3),
+        "contiguous": {
+            "what": "the same step and the same K/V rows with contiguous placement: "
+                    "step_us = mlr_paged_decode_append with each sequence's blocks consecutive "
+                    "in the pool; floor_seq_us = the read floor on those tables (96-token "
+                    "items); floor_flat_us = the read floor over the same number of token "
+                    "rows as one run of consecutive blocks (one sequence)",
+            "step_us": round(res["contig"] * 1e6, 3),
+            "floor_seq_us": round(res["floor_seq"] * 1e6, 3),
+            "floor_flat_us": round(res["floor_flat"] * 1e6, 3),
+            "floor_flat_frac_of_hbm_peak": round(
+                kv_bytes / res["floor_flat"] / 1e9 / HBM_PEAK_GBS, 4),
+        },
     }
     return {
         "wl": wl,

@@ -26,9 +26,16 @@ import torch
 from . import paged_attention as pa
 
 
-def rope_tables(positions: torch.Tensor, head_dim: int, theta: float, dtype):
-    """cos, sin [..., D] for integer positions (reference :125-170)."""
+def rope_tables(positions: torch.Tensor, head_dim: int, theta: float, dtype,
+                freq_dtype: torch.dtype | None = None):
+    """cos, sin [..., D] for integer positions (reference :125-170).
+
+    inv_freq is an FP32 buffer of the rotary module (:135-141); a module cast
+    with .to(freq_dtype) holds it rounded to that dtype, and the FP32
+    positions then multiply the rounded values (type promotion, :164-167)."""
     inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    if freq_dtype is not None:
+        inv_freq = inv_freq.to(freq_dtype).to(torch.float32)
     angles = positions.to(torch.float32).unsqueeze(-1) * inv_freq
     angles = torch.cat((angles, angles), dim=-1)
     return angles.cos().to(dtype), angles.sin().to(dtype)
@@ -49,10 +56,17 @@ def project(hidden: torch.Tensor, w: dict, hq: int, hkv: int, d: int):
     return q, k, v
 
 
-def qkv_rope(hidden, positions, w, hq, hkv, d, theta):
+def qkv_rope(hidden, positions, w, hq, hkv, d, theta, freq_dtype=None):
     q, k, v = project(hidden, w, hq, hkv, d)
-    cos, sin = rope_tables(positions, d, theta, hidden.dtype)
+    cos, sin = rope_tables(positions, d, theta, hidden.dtype, freq_dtype)
     return rotate(q, cos, sin), rotate(k, cos, sin), v
+
+
+def _unpack(cfg):
+    """cfg = (hq, hkv, d, theta) or (hq, hkv, d, theta, freq_dtype): the last
+    is the dtype the rotary module was cast to (None or absent: FP32)."""
+    hq, hkv, d, theta, *rest = cfg
+    return hq, hkv, d, theta, (rest[0] if rest else None)
 
 
 def dense_causal(q, k, v, scale):
@@ -71,16 +85,16 @@ def dense_causal(q, k, v, scale):
 
 
 def prefill_whole(hidden, positions, cache, layer, slots, w, cfg):
-    hq, hkv, d, theta = cfg
-    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta)
+    hq, hkv, d, theta, fdt = _unpack(cfg)
+    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta, fdt)
     cache.write_slots(slots, k.squeeze(0), v.squeeze(0), layer)
     out = dense_causal(q, k, v, d ** -0.5)
     return torch.nn.functional.linear(out, w["o_w"])
 
 
 def decode_single(hidden, positions, cache, layer, slots, block_table, context_len, w, cfg):
-    hq, hkv, d, theta = cfg
-    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta)
+    hq, hkv, d, theta, fdt = _unpack(cfg)
+    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta, fdt)
     cache.write_slots(slots, k.squeeze(1), v.squeeze(1), layer)
     kc, vc = cache.get_layer_cache(layer)
     out = pa.decode_single(q[0, 0], kc, vc, block_table, context_len, cache.block_size)
@@ -88,9 +102,9 @@ def decode_single(hidden, positions, cache, layer, slots, block_table, context_l
 
 
 def decode_batch(hidden, positions, cache, layer, slots, block_tables, context_lens, w, cfg):
-    hq, hkv, d, theta = cfg
+    hq, hkv, d, theta, fdt = _unpack(cfg)
     batch = hidden.shape[0]
-    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta)
+    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta, fdt)
     cache.write_slots(slots, k.squeeze(1), v.squeeze(1), layer)
     kc, vc = cache.get_layer_cache(layer)
     out = pa.decode_batch_parallel(q.squeeze(1), kc, vc, block_tables, context_lens,
@@ -100,9 +114,9 @@ def decode_batch(hidden, positions, cache, layer, slots, block_tables, context_l
 
 def prefill_chunk(hidden, positions, cache, layer, slots, block_table, prefix_len,
                   context_len, tile_size, w, cfg):
-    hq, hkv, d, theta = cfg
+    hq, hkv, d, theta, fdt = _unpack(cfg)
     chunk = hidden.shape[1]
-    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta)
+    q, k, v = qkv_rope(hidden, positions, w, hq, hkv, d, theta, fdt)
     cache.write_slots(slots, k.squeeze(0), v.squeeze(0), layer)
     kc, vc = cache.get_layer_cache(layer)
     out = pa.prefill_chunk_tiled(q.squeeze(0), kc, vc, block_table, prefix_len, context_len,

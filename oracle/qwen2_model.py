@@ -49,6 +49,9 @@ class OracleQwen2:
         self.cfg = config
         self.dims = (config.num_attention_heads, config.num_key_value_heads,
                      config.head_dim, config.rope_theta)
+        # A reference model cast with .to(dtype) holds its rotary inv_freq
+        # buffers in that dtype (qwen2_attention.rope_tables).
+        self.freq_dtype = dtype
         self.embed = sd["model.embed_tokens.weight"]
         self.norm_w = sd["model.norm.weight"]
         self.lm_head = sd.get("lm_head.weight", self.embed)
@@ -86,7 +89,7 @@ class OracleQwen2:
         h = F.embedding(ids, self.embed)
         for layer in self.layers:
             x = rms_norm(h, layer["in_norm"], self.cfg.rms_norm_eps)
-            q, k, v = qa.qkv_rope(x, pos, layer["attn"], hq, hkv, d, theta)
+            q, k, v = qa.qkv_rope(x, pos, layer["attn"], hq, hkv, d, theta, self.freq_dtype)
             h = h + F.linear(qa.dense_causal(q, k, v, d ** -0.5), layer["attn"]["o_w"])
             h = self._mlp_block(h, layer)
         return self._logits(h)[0]
@@ -98,6 +101,47 @@ class OracleQwen2:
             out.append(nxt)
             tokens.append(nxt)
         return out
+
+    def _prompt_pass(self, prompt: list[int]):
+        """The prompt in one dense causal pass: the logits row of its last
+        position, and per layer the contiguous K/V rows [T, Hkv, D]."""
+        hq, hkv, d, theta = self.dims
+        ks: list[torch.Tensor] = []
+        vs: list[torch.Tensor] = []
+        ids = torch.tensor([prompt], dtype=torch.long)
+        pos = torch.arange(len(prompt), dtype=torch.long).unsqueeze(0)
+        h = F.embedding(ids, self.embed)
+        for layer in self.layers:
+            x = rms_norm(h, layer["in_norm"], self.cfg.rms_norm_eps)
+            q, k, v = qa.qkv_rope(x, pos, layer["attn"], hq, hkv, d, theta, self.freq_dtype)
+            ks.append(k[0])
+            vs.append(v[0])
+            h = h + F.linear(qa.dense_causal(q, k, v, d ** -0.5), layer["attn"]["o_w"])
+            h = self._mlp_block(h, layer)
+        return self._logits(h)[0, -1], ks, vs
+
+    def _decode_row(self, token: int, p: int, ks: list, vs: list) -> torch.Tensor:
+        """One decode step: `token` at position `p` attends over every K/V row
+        so far plus its own (appended to ks/vs); its logits row."""
+        hq, hkv, d, theta = self.dims
+        group, scale = hq // hkv, d ** -0.5
+        h = F.embedding(torch.tensor([[token]]), self.embed)
+        posn = torch.tensor([[p]], dtype=torch.long)
+        for i, layer in enumerate(self.layers):
+            x = rms_norm(h, layer["in_norm"], self.cfg.rms_norm_eps)
+            q, k, v = qa.qkv_rope(x, posn, layer["attn"], hq, hkv, d, theta, self.freq_dtype)
+            ks[i] = torch.cat([ks[i], k[0]])
+            vs[i] = torch.cat([vs[i], v[0]])
+            kk = ks[i].repeat_interleave(group, dim=-2).transpose(0, 1)   # [Hq, T, D]
+            vv = vs[i].repeat_interleave(group, dim=-2).transpose(0, 1)
+            scores = (q[0, 0].unsqueeze(1) @ kk.transpose(-2, -1)) * scale  # [Hq, 1, T]
+            sm = torch.float32 if scores.dtype in (torch.float16, torch.bfloat16) \
+                else scores.dtype
+            probs = torch.softmax(scores, dim=-1, dtype=sm).to(vv.dtype)
+            att = (probs @ vv).reshape(1, 1, hq * d)
+            h = h + F.linear(att, layer["attn"]["o_w"])
+            h = self._mlp_block(h, layer)
+        return self._logits(h)[0, -1]
 
     def cached_greedy(self, prompt: list[int], max_new_tokens: int,
                       margins: list | None = None) -> list[int]:
@@ -112,38 +156,20 @@ class OracleQwen2:
                 margins.append((float(top.values[0] - top.values[1]), int(top.indices[1])))
             return int(top.indices[0])
 
-        hq, hkv, d, theta = self.dims
-        group, scale = hq // hkv, d ** -0.5
-        ks: list[torch.Tensor] = []
-        vs: list[torch.Tensor] = []
-        ids = torch.tensor([prompt], dtype=torch.long)
-        pos = torch.arange(len(prompt), dtype=torch.long).unsqueeze(0)
-        h = F.embedding(ids, self.embed)
-        for layer in self.layers:
-            x = rms_norm(h, layer["in_norm"], self.cfg.rms_norm_eps)
-            q, k, v = qa.qkv_rope(x, pos, layer["attn"], hq, hkv, d, theta)
-            ks.append(k[0])
-            vs.append(v[0])
-            h = h + F.linear(qa.dense_causal(q, k, v, scale), layer["attn"]["o_w"])
-            h = self._mlp_block(h, layer)
-        out = [pick(self._logits(h)[0, -1])]
+        row, ks, vs = self._prompt_pass(prompt)
+        out = [pick(row)]
         while len(out) < max_new_tokens:
-            p = len(prompt) + len(out) - 1
-            h = F.embedding(torch.tensor([[out[-1]]]), self.embed)
-            posn = torch.tensor([[p]], dtype=torch.long)
-            for i, layer in enumerate(self.layers):
-                x = rms_norm(h, layer["in_norm"], self.cfg.rms_norm_eps)
-                q, k, v = qa.qkv_rope(x, posn, layer["attn"], hq, hkv, d, theta)
-                ks[i] = torch.cat([ks[i], k[0]])
-                vs[i] = torch.cat([vs[i], v[0]])
-                kk = ks[i].repeat_interleave(group, dim=-2).transpose(0, 1)   # [Hq, T, D]
-                vv = vs[i].repeat_interleave(group, dim=-2).transpose(0, 1)
-                scores = (q[0, 0].unsqueeze(1) @ kk.transpose(-2, -1)) * scale  # [Hq, 1, T]
-                sm = torch.float32 if scores.dtype in (torch.float16, torch.bfloat16) \
-                    else scores.dtype
-                probs = torch.softmax(scores, dim=-1, dtype=sm).to(vv.dtype)
-                att = (probs @ vv).reshape(1, 1, hq * d)
-                h = h + F.linear(att, layer["attn"]["o_w"])
-                h = self._mlp_block(h, layer)
-            out.append(pick(self._logits(h)[0, -1]))
+            out.append(pick(self._decode_row(out[-1], len(prompt) + len(out) - 1, ks, vs)))
         return out
+
+    def teacher_forced_logits(self, prompt: list[int], forced: list[int]) -> torch.Tensor:
+        """Logits rows [1 + len(forced), vocab]: the prompt's last position,
+        then the row of each forced token fed in turn at the next position
+        (whatever the model would have picked), as the reference's batch
+        decode test drives its model (tests/model/test_qwen2_batch_decode.py:
+        100-170)."""
+        row, ks, vs = self._prompt_pass(prompt)
+        rows = [row]
+        for i, token in enumerate(forced):
+            rows.append(self._decode_row(token, len(prompt) + i, ks, vs))
+        return torch.stack(rows)

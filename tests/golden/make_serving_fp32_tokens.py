@@ -1,9 +1,10 @@
-"""Expected FP32 greedy tokens of sampled requests of the Qwen2.5-0.5B-shape
+"""Expected FP32 greedy tokens of the requests of the Qwen2.5-0.5B-shape
 serving workload (workloads.qwen05b_serving), from the oracle on the CPU.
 
     python tests/golden/make_serving_fp32_tokens.py
 
-writes tests/golden/serving_qwen05b_fp32_tokens.json: per sampled request its
+writes tests/golden/serving_qwen05b_fp32_tokens.json: per request (all 48
+initial requests and the first eight arrivals) its
 id, prompt length, the oracle's greedy tokens for all max_new_tokens, and per
 step the top-2 logit margin and the second-best token. At each near tie
 (margin below NEAR_TIE) it also stores the branch: the oracle's greedy tokens
@@ -31,9 +32,9 @@ from mini_llm_runtime_amd import workloads  # noqa: E402
 from mini_llm_runtime_amd.model.qwen2 import TinyQwen2Config, TinyQwen2ForCausalLM  # noqa: E402
 from oracle.qwen2_model import OracleQwen2  # noqa: E402
 
-# Every sixth initial request and the first eight arrivals (all of them are
+# Every initial request and the first eight arrivals (all of them are
 # admitted during the warm-up or early in the measured steps).
-SAMPLED = [f"init{i}" for i in range(0, 48, 6)] + [f"arr{i}" for i in range(8)]
+SAMPLED = [f"init{i}" for i in range(48)] + [f"arr{i}" for i in range(8)]
 OUT = os.path.join(HERE, "serving_qwen05b_fp32_tokens.json")
 NEAR_TIE = 1e-3  # must equal tests/test_gpu_runtime.py's NEAR_TIE
 

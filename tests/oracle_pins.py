@@ -404,6 +404,11 @@ def check_model_vs_textbook(mod):
         assert cached[step] == int(order[0])
         assert abs(margins[step][0] - (row[order[0]] - row[order[1]])) < 1e-6
         seq.append(cached[step])
+    # Teacher forcing: tokens the model would not pick, fed one per step.
+    forced = torch.randint(0, MODEL_CFG.vocab_size, (5,), generator=gen).tolist()
+    rows = oracle.teacher_forced_logits(prompt, forced).numpy()
+    np.testing.assert_allclose(rows, np_model_logits(sd, prompt + forced)[len(prompt) - 1:],
+                               rtol=1e-6, atol=1e-6)
 
 
 MODEL_CHECKS = (check_model_vs_textbook,)

@@ -41,8 +41,12 @@ def make_module(cfg, dtype, device, seed=0):
     return module.to(device), w
 
 
-def oracle_cfg(cfg):
-    return (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rope_theta)
+def oracle_cfg(cfg, dtype):
+    """The oracle's (hq, hkv, d, theta, freq_dtype): make_module casts the
+    module to `dtype`, and with it the rotary inv_freq buffer, as a reference
+    module cast with .to(dtype) holds it."""
+    return (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rope_theta,
+            dtype)
 
 
 def paired_caches(cfg, dtype, device, num_blocks, bs, seed):
@@ -129,7 +133,7 @@ def test_decode_batch_with_cache(device, cfg, dtype):
     dev, ora = paired_caches(cfg, dtype, device, nblocks, bs, seed=5)
     got = module.forward_decode_batch_with_cache(hidden.to(device), pos.to(device), dev, 0,
                                                  slots.to(device), bt.to(device), ctx.to(device))
-    want = oqa.decode_batch(hidden, pos, ora, 0, slots, bt, ctx, w, oracle_cfg(cfg))
+    want = oqa.decode_batch(hidden, pos, ora, 0, slots, bt, ctx, w, oracle_cfg(cfg, dtype))
     print(f"decode batch {cfg.hidden_size} {dtype}: max-abs {max_abs(got, want):.3e}")
     assert max_abs(got, want) <= TOL[dtype]
     check_caches(dev, ora, slots.tolist(), *module_rows(module, hidden, pos, device))
@@ -149,7 +153,7 @@ def test_decode_single_with_cache(device, cfg, dtype):
     dev, ora = paired_caches(cfg, dtype, device, nblocks, bs, seed=6)
     got = module.forward_decode_with_cache(hidden.to(device), pos.to(device), dev, 0,
                                            slot.to(device), table, n)
-    want = oqa.decode_single(hidden, pos, ora, 0, slot, table, n, w, oracle_cfg(cfg))
+    want = oqa.decode_single(hidden, pos, ora, 0, slot, table, n, w, oracle_cfg(cfg, dtype))
     assert max_abs(got, want) <= TOL[dtype]
     check_caches(dev, ora, slot.tolist(), *module_rows(module, hidden, pos, device))
 
@@ -176,7 +180,7 @@ def test_prefill_chunk_with_cache(device, cfg, dtype, prefix, chunk, tile):
                                                   0, slots.to(device), table, prefix, context,
                                                   tile)
     want = oqa.prefill_chunk(hidden, positions, ora, 0, slots, table, prefix, context, tile, w,
-                             oracle_cfg(cfg))
+                             oracle_cfg(cfg, dtype))
     print(f"prefill chunk {cfg.hidden_size} {dtype} p{prefix} c{chunk}: "
           f"max-abs {max_abs(got, want):.3e}")
     assert max_abs(got, want) <= TOL[dtype]
@@ -197,7 +201,7 @@ def test_prefill_whole_with_cache(device, cfg, dtype, seq):
     dev, ora = paired_caches(cfg, dtype, device, nblocks, bs, seed=4)
     got = module.forward_prefill_with_cache(hidden.to(device), positions.to(device), dev, 0,
                                             slots.to(device))
-    want = oqa.prefill_whole(hidden, positions, ora, 0, slots, w, oracle_cfg(cfg))
+    want = oqa.prefill_whole(hidden, positions, ora, 0, slots, w, oracle_cfg(cfg, dtype))
     assert max_abs(got, want) <= TOL[dtype]
     check_caches(dev, ora, slots.tolist(),
                  *module_rows(module, hidden, positions, device, fused=False))
@@ -219,7 +223,7 @@ def test_decode_steps_follow_the_prefill(device):
     positions = torch.arange(prompt).unsqueeze(0)
     got = module.forward_prefill_with_cache(hidden.to(device), positions.to(device), dev, 0,
                                             slots.to(device))
-    want = oqa.prefill_whole(hidden, positions, ora, 0, slots, w, oracle_cfg(cfg))
+    want = oqa.prefill_whole(hidden, positions, ora, 0, slots, w, oracle_cfg(cfg, dtype))
     assert max_abs(got, want) <= TOL[dtype]
     written = slots.tolist()
     rows = [module_rows(module, hidden, positions, device, fused=False)]
@@ -233,7 +237,7 @@ def test_decode_steps_follow_the_prefill(device):
         got = module.forward_decode_batch_with_cache(x.to(device), pos.to(device), dev, 0,
                                                      slot.to(device), bt.to(device),
                                                      ctx.to(device))
-        want = oqa.decode_batch(x, pos, ora, 0, slot, bt, ctx, w, oracle_cfg(cfg))
+        want = oqa.decode_batch(x, pos, ora, 0, slot, bt, ctx, w, oracle_cfg(cfg, dtype))
         assert max_abs(got, want) <= TOL[dtype], f"step {step}"
         written += slot.tolist()
         rows.append(module_rows(module, x, pos, device))

@@ -235,7 +235,8 @@ def test_qwen05b_serving_fp32_matches_oracle_tokens(device):
     """The Qwen2.5-0.5B-shape serving workload (24 layers; 48 decoding
     requests with prompts U[64, 2048], 1024-token prompts arriving, about 48
     decodes + 2 prefills per step) in FP32: the warm-up, then 128 steps. The
-    sampled requests' tokens equal the oracle's greedy tokens
+    tokens of all 48 initial requests and of the first eight arrivals (1,413
+    tokens) equal the oracle's greedy tokens
     (tests/golden/serving_qwen05b_fp32_tokens.json, from
     tests/golden/make_serving_fp32_tokens.py), up to the near-tie rule."""
     import json
@@ -273,4 +274,7 @@ def test_qwen05b_serving_fp32_matches_oracle_tokens(device):
     uncompared = sum(left for rid, *_, left in exemptions if "/" not in rid)
     print(f"serving fp32: {compared} tokens identical to the oracle's, "
           f"{len(exemptions)} near-tie exemption(s), {uncompared} tokens not compared")
-    assert compared >= 200
+    total = sum(len(g["tokens"]) for g in golden["requests"])
+    assert all(len(by_id[g["request_id"]].output_token_ids) == len(g["tokens"])
+               for g in golden["requests"])  # every golden request ran to its end
+    assert compared >= 0.95 * total

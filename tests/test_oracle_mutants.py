@@ -131,9 +131,13 @@ MODEL_MUTATIONS = {
         "return F.linear(rms_norm(h, self.norm_w, self.cfg.rms_norm_eps), self.lm_head)",
         "return F.linear(h, self.lm_head)",
     ),
-    "cached-decode-position-off-by-one": (
-        "p = len(prompt) + len(out) - 1",
-        "p = len(prompt) + len(out)",
+    "decode-row-position-off-by-one": (
+        "posn = torch.tensor([[p]], dtype=torch.long)",
+        "posn = torch.tensor([[p + 1]], dtype=torch.long)",
+    ),
+    "teacher-forced-row-skipped": (
+        "rows.append(self._decode_row(token, len(prompt) + i, ks, vs))",
+        "rows.append(self._decode_row(token, len(prompt) + i + 1, ks, vs))",
     ),
 }
 

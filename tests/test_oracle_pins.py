@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -104,3 +105,24 @@ def test_slot_formula_and_padding():
 def test_oracle_model_is_pinned(check):
     import oracle.qwen2_model as qm
     check(qm)
+
+
+def test_rope_tables_of_a_cast_module_use_rounded_frequencies():
+    """A reference rotary module cast with .to(torch.bfloat16) holds its
+    inv_freq buffer in bf16 (registered at model/qwen2.py:135-141), and the
+    FP32 positions multiply those rounded values (:164-167). Pinned against
+    float64 arithmetic on the rounded frequencies, and shown to differ from
+    the FP32-frequency tables at long positions (so the test tells them apart)."""
+    import oracle.qwen2_attention as oqa
+
+    pos = torch.tensor([0, 1, 7, 100, 1000])
+    cos, sin = oqa.rope_tables(pos, 64, 1e6, torch.float32, freq_dtype=torch.bfloat16)
+    inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+    inv = inv.to(torch.bfloat16).double().numpy()
+    angles = pos.double().numpy()[:, None] * inv
+    angles = np.concatenate([angles, angles], axis=-1)
+    # FP32 rounding of an angle of up to 1000 rad moves it by at most 3e-5.
+    np.testing.assert_allclose(cos.numpy(), np.cos(angles), atol=1e-4)
+    np.testing.assert_allclose(sin.numpy(), np.sin(angles), atol=1e-4)
+    cos32, _ = oqa.rope_tables(pos, 64, 1e6, torch.float32)
+    assert (cos32[-1] - cos[-1]).abs().max().item() > 1e-2
