@@ -5,7 +5,8 @@
  * mini-llm-runtime on gfx950 (MI355X):
  *   1. the KV-cache write: a slot_mapping scatter into one layer's block pool;
  *   2. batched single-token paged decode (split-KV; the splits merge in the
- *      same launch on the bf16 matrix-core path, in a second one otherwise);
+ *      same launch on the bf16 and FP32 matrix-core paths, in a second one
+ *      otherwise);
  *   3. paged chunk-prefill attention (causal by absolute token position).
  *
  * Conventions shared by every entry point:
@@ -92,10 +93,12 @@ int mlr_kv_write(const void *k, const void *v, int src_dtype,
  * Bytes of workspace mlr_paged_decode needs for these sizes. `max_context`
  * bounds every context length (the host passes block_table width * block_size).
  * tokens_per_split <= 0 sizes for the library's default splits, whichever
- * kernel the call takes. The defaults: bf16 head_dim 64/128 (matrix-core
- * kernel) 320 tokens at head_dim 64 when max_context <= 5120, else
- * max(256, ceil(max_context / 16)) rounded up to a multiple of 256; other
- * dtypes and shapes an eighth of max_context as a power of two in [32, 256].
+ * kernel the call takes. The defaults: bf16 and FP32 with head_dim 64/128, at
+ * most 16 query heads per KV head and block_size a multiple of 16
+ * (matrix-core kernel): 320 tokens for bf16 head_dim 64 when max_context <=
+ * 5120, else max(256, ceil(max_context / 16)) rounded up to a multiple of
+ * 256; other dtypes and shapes an eighth of max_context as a power of two in
+ * [32, 256].
  */
 size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
                                        int64_t head_dim, int64_t max_context,
@@ -118,8 +121,8 @@ size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
  *   tokens_per_split: split-KV granularity in tokens (<= 0: library default)
  *   workspace    : >= mlr_paged_decode_workspace_size(...) bytes, 256-aligned,
  *                  all-zero before its first use (hipMemset once). It holds
- *                  the splits' partial results; the bf16 matrix-core kernel
- *                  merges them in the same launch (the workgroup of a
+ *                  the splits' partial results; the matrix-core kernel (bf16
+ *                  and FP32) merges them in the same launch (the workgroup of a
  *                  sequence's last split waits for the words of the others
  *                  to arrive, a zero word meaning "not yet"). Every call
  *                  returns each word it wrote to zero, so the workspace can be
@@ -152,9 +155,10 @@ int mlr_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
  * mlr_kv_write(new_k, new_v, slot_mapping) followed by mlr_paged_decode(...)
  * when, as the reference requires of a decode step, slot_mapping[b] is the slot
  * of position context_lens[b] - 1 and the slots are distinct
- * (model/qwen2.py:595-602). The bf16 kernel writes the rows and uses them from
- * registers, saving the separate write kernel; other dtypes run the two
- * kernels in sequence.
+ * (model/qwen2.py:595-602). The matrix-core kernel (bf16 and FP32, the shapes
+ * of mlr_paged_decode's defaults) writes the rows and uses them from LDS,
+ * saving the separate write kernel; other dtypes and shapes run the write
+ * kernel, then the decode.
  *
  * Replaces the write_slots + paged_attention_decode_batch_parallel pair of
  * Qwen2Attention.forward_decode_batch_with_cache (model/qwen2.py:608-621).
@@ -232,7 +236,7 @@ int mlr_paged_decode_append_static(
     int64_t out_stride_b, int64_t out_stride_h, void *stream);
 
 /*
- * Merge-failure check of a decode workspace, and its recovery. The bf16
+ * Merge-failure check of a decode workspace, and its recovery. The
  * single-launch merge of mlr_paged_decode and its variants waits only for
  * workgroups launched before its own, with a bounded wait; should that wait
  * ever give up, the merge sets the workspace's flag word and writes NaN, and

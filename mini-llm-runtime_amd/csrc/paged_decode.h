@@ -31,6 +31,7 @@ struct DecodeParams {
   float2 *ws_ml;   // [batch][hq][max_splits] = (m, l)
   void *ws_acc;    // [batch][hq][max_splits][d], FP32 (FP64 for f64 inputs)
   int ml_base2;    // 1: m is a base-2 exponent, 0: natural-log units
+  int dtype;       // mlr_dtype of q, the cache and out
   void *out;
   int64_t o_sb, o_sh;
   // Fused KV write (mlr_paged_decode_append); new_k == nullptr: none.
@@ -64,11 +65,11 @@ struct DecodeWorkspace {
 // fifth tile in LDS.
 constexpr int kLdsSplit64 = 320;
 
-int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_context);
+int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_context, int dtype);
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype);
 
-// bf16, head_dim 64/128, GQA group <= 16 and block_size a multiple of 16.
+// bf16 or FP32, head_dim 64/128, GQA group <= 16 and block_size a multiple of 16.
 bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
                           int64_t block_size);
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream);

@@ -14,9 +14,10 @@
 // scale (rounded again), then an FP32 softmax over positions t < seq_len;
 // positions past seq_len and padded block-table entries never contribute.
 //
-// bf16 inputs with head_dim 64 or 128 and at most 16 query heads per KV head
-// take the MFMA kernel in paged_decode_mfma.hip; everything else takes the
-// generic kernel below.
+// bf16 and FP32 inputs with head_dim 64 or 128, at most 16 query heads per KV
+// head and block_size a multiple of 16 take the matrix-core kernel in
+// paged_decode_mfma.hip (one launch, splits merged in it); everything else
+// takes the generic kernels below.
 #include <algorithm>
 #include <atomic>
 
@@ -260,23 +261,25 @@ int launch_combine(const DecodeParams &p, hipStream_t stream) {
 
 template int launch_combine<bf16_t>(const DecodeParams &, hipStream_t);
 
-int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_context) {
+int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_context, int dtype) {
   // Generic kernel: an eighth of the longest context, as a power of two in
   // [32, 256] (its scores are held in LDS), so that short contexts still
   // spread over several workgroups per (sequence, KV head). Matrix-core
   // kernel at head_dim 64 with contexts of up to 16 x 320 tokens: 320 (four
   // tiles per wave in registers and one in LDS), so a batch of long contexts
   // fits the GPU in one generation of workgroups. Otherwise at least 256
-  // tokens (16 tiles, four per wave, loaded in one batch), and at most 16
-  // splits per sequence: long contexts then get fewer, longer splits
-  // (measured at 8 x 32K tokens: 133 us with 128 splits, 108-111 us with
-  // 8-16), and the merge takes every sequence in one 16-split chunk.
+  // tokens (16 tiles, four per wave, loaded in one batch; FP32 tiles go two
+  // or one per batch), and at most 16 splits per sequence: long contexts
+  // then get fewer, longer splits (measured at 8 x 32K tokens: 133 us with
+  // 128 splits, 108-111 us with 8-16), and the merge takes every sequence in
+  // one 16-split chunk.
   if (!mfma) {
     int64_t ts = 32;
     while (ts < 256 && ts * 8 < max_context) ts *= 2;
     return ts;
   }
-  if (head_dim == 64 && max_context <= 16 * kLdsSplit64) return kLdsSplit64;
+  if (dtype == MLR_DTYPE_BF16 && head_dim == 64 && max_context <= 16 * kLdsSplit64)
+    return kLdsSplit64;
   const int64_t per16 = ceil_div(max_context, 16);
   return per16 <= 256 ? 256 : ceil_div(per16, 256) * 256;
 }
@@ -309,7 +312,7 @@ extern "C" size_t mlr_paged_decode_workspace_size(int64_t batch,
   // kernel uses by default, so it covers whichever kernel the call takes.
   const int64_t ts = tokens_per_split > 0
                          ? tokens_per_split
-                         : default_tokens_per_split(false, head_dim, max_context);
+                         : default_tokens_per_split(false, head_dim, max_context, dtype);
   const int64_t splits = ceil_div(max_context, ts);
   return static_cast<size_t>(
       decode_workspace_layout(batch, num_q_heads, head_dim, splits, dtype).total);
@@ -367,7 +370,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
       aligned && max_context < (int64_t(1) << 31) &&
       decode_mfma_eligible(dtype, head_dim, num_q_heads / num_kv_heads, block_size);
   int64_t ts = tokens_per_split > 0 ? tokens_per_split
-                                    : default_tokens_per_split(mfma, head_dim, max_context);
+                                    : default_tokens_per_split(mfma, head_dim, max_context, dtype);
   if (!mfma) {
     MLR_REQUIRE(ts <= kGenMaxSplit,
                 "mlr_paged_decode: tokens_per_split %lld exceeds %d for this "
@@ -418,6 +421,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
   p.ws_ml = reinterpret_cast<float2 *>(static_cast<unsigned char *>(workspace) + wl.ml_offset);
   p.ws_acc = static_cast<unsigned char *>(workspace) + wl.acc_offset;
   p.ml_base2 = mfma ? 1 : 0;
+  p.dtype = dtype;
   p.out = out;
   p.o_sb = out_stride_b;
   p.o_sh = out_stride_h;
@@ -432,7 +436,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                               app->sb % 8 == 0 && app->sh % 8 == 0;
     if (app->inv_freq != nullptr) {
       // The fused rotary embedding exists on the matrix-core kernel only.
-      MLR_REQUIRE(mfma && rows_aligned,
+      MLR_REQUIRE(mfma && dtype == MLR_DTYPE_BF16 && rows_aligned,
                   "mlr_paged_decode_qkv: needs bf16, head_dim 64 or 128, at most 16 query "
                   "heads per KV head, block_size a multiple of 16 and 16-byte aligned rows");
       p.inv_freq = app->inv_freq;

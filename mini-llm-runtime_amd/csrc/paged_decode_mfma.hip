@@ -1,4 +1,4 @@
-// bf16 split-KV paged decode on gfx950 matrix cores, in one launch.
+// bf16 and FP32 split-KV paged decode on gfx950 matrix cores, in one launch.
 //
 // One workgroup of four wavefronts per (live split, KV head), or of eight per
 // (live split, pair of KV heads), four for each head. A split is
@@ -48,6 +48,12 @@
 // Scores are rounded like the reference's bf16 matmul (to bf16, times scale,
 // to bf16 again: kernels/reference/paged_attention.py:246-247) before the
 // FP32 softmax (:251).
+//
+// FP32 inputs take the same kernel with v_mfma_f32_16x16x4_f32 in place of
+// the bf16 instructions (compute_tile for Tile<float, D>): its 16x16
+// accumulator has the bf16 tiles' layout, so the softmax, the merges, the
+// work items and the fused KV write are shared. Scores, probabilities and
+// P@V stay FP32, as in the reference's FP32 path.
 #include "paged_decode.h"
 
 namespace mlr {
@@ -63,6 +69,29 @@ constexpr float kLog2e = 1.4426950408889634f;
 template <int D> struct VRow;
 template <> struct VRow<64> { using type = uint2; };   // 4 bf16 per lane
 template <> struct VRow<128> { using type = uint4; };  // 8 bf16 per lane
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+
+// What one lane holds of a 16-token tile, by element type (bf16_t or float):
+// K as kKChunks 16-byte chunks of token l%16's row (8 bf16 or 4 floats each:
+// the elements 4 kE j + kE g .. + kE of chunk j, kE = 16 / element size,
+// g = l/16), and V as rows 4g .. 4g + 3, D/16 elements each (VT).
+template <typename T, int D> struct TileTraits;
+template <int D> struct TileTraits<bf16_t, D> {
+  static constexpr int kKChunks = D / 32;
+  using VT = typename VRow<D>::type;
+  using S = uint16_t;  // storage element
+};
+template <> struct TileTraits<float, 64> {
+  static constexpr int kKChunks = 4;
+  using VT = uint4;
+  using S = float;
+};
+template <> struct TileTraits<float, 128> {
+  static constexpr int kKChunks = 8;
+  using VT = u32x8_t;
+  using S = float;
+};
 
 // a and b rounded to bf16 (nearest even) and back to FP32, with one
 // v_cvt_pk_bf16_f32 for the pair.
@@ -172,10 +201,10 @@ __device__ __forceinline__ T select_vec(bool c, const T &a, const T &b) {
 }
 
 // Registers of one loaded tile. blk and rel are wave-uniform.
-template <int D>
+template <typename T, int D>
 struct Tile {
-  uint4 k[D / 32];
-  typename VRow<D>::type v[4];
+  uint4 k[TileTraits<T, D>::kKChunks];
+  typename TileTraits<T, D>::VT v[4];
   int blk;  // physical block id, -1 when the tile is absent or invalid
   int rel;  // position of the tile's first token relative to the split start
   int sub;  // row (0..15) whose K/V the appended token replaces, or -1
@@ -189,27 +218,27 @@ struct DecodeState {
 
 // Per-lane byte offsets inside a 16-token tile, fixed for the whole kernel.
 struct LaneOffsets {
-  int k;       // K row of token m16, dims 8g..: ((m16 * hkv + kvh) * D + 8g) * 2
-  int v;       // V row of token 4g, dims VC*m16..: ((4g * hkv + kvh) * D + VC*m16) * 2
-  int v_step;  // bytes between consecutive token rows (hkv * D * 2)
+  int k;       // K row of token m16, chunk 0 of lane group g: ((m16 * hkv + kvh) * D) * size + 16g
+  int v;       // V row of token 4g, dims VC*m16..: ((4g * hkv + kvh) * D + VC*m16) * size
+  int v_step;  // bytes between consecutive token rows (hkv * D * size)
 };
 
 // Raw buffer resource over one physical block (gfx9 descriptor word 3). The
 // base is wave-uniform, so the loads use a scalar descriptor plus 32-bit lane
 // offsets, and the hardware drops any access outside the block.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const uint16_t *base,
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const void *base,
                                                              uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes,
-                                           0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
 }
 
-template <int D>
-__device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
-                                          const uint16_t *vc, int64_t block_elems,
-                                          int tile_off_bytes, int blk, int rel,
-                                          const LaneOffsets &o) {
-  constexpr int QK = D / 32;
-  using VT = typename VRow<D>::type;
+template <typename T, int D>
+__device__ __forceinline__ void load_tile(Tile<T, D> &t, const typename TileTraits<T, D>::S *kc,
+                                          const typename TileTraits<T, D>::S *vc,
+                                          int64_t block_elems, int tile_off_bytes, int blk,
+                                          int rel, const LaneOffsets &o) {
+  constexpr int QK = TileTraits<T, D>::kKChunks;
+  using VT = typename TileTraits<T, D>::VT;
+  constexpr int kSize = static_cast<int>(sizeof(T));
   t.blk = blk;
   t.rel = rel;
   t.sub = -1;
@@ -218,7 +247,7 @@ __device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
   // the compiler's wait counts assume the fewest loads on any path, so the
   // first tile would wait for nearly every load of the batch.
   const bool ok = blk >= 0;
-  const uint32_t bytes = ok ? static_cast<uint32_t>(block_elems * 2) : 0u;
+  const uint32_t bytes = ok ? static_cast<uint32_t>(block_elems * kSize) : 0u;
   const int64_t base = ok ? (int64_t)blk * block_elems : 0;
   const __amdgpu_buffer_rsrc_t rk = block_rsrc(kc + base, bytes);
   const __amdgpu_buffer_rsrc_t rv = block_rsrc(vc + base, bytes);
@@ -228,12 +257,19 @@ __device__ __forceinline__ void load_tile(Tile<D> &t, const uint16_t *kc,
         uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, o.k + 64 * j, tile_off_bytes, 0));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if constexpr (D == 64) {
+    if constexpr (sizeof(VT) == 8) {
       t.v[i] = __builtin_bit_cast(
           VT, __builtin_amdgcn_raw_buffer_load_b64(rv, o.v + i * o.v_step, tile_off_bytes, 0));
-    } else {
+    } else if constexpr (sizeof(VT) == 16) {
       t.v[i] = __builtin_bit_cast(
           VT, __builtin_amdgcn_raw_buffer_load_b128(rv, o.v + i * o.v_step, tile_off_bytes, 0));
+    } else {  // 32 bytes: two loads
+      const uint4 lo = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, o.v + i * o.v_step, tile_off_bytes, 0));
+      const uint4 hi = __builtin_bit_cast(
+          uint4,
+          __builtin_amdgcn_raw_buffer_load_b128(rv, o.v + i * o.v_step + 16, tile_off_bytes, 0));
+      t.v[i] = VT{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     }
   }
 }
@@ -272,7 +308,7 @@ __device__ __forceinline__ void copy_tile_to_lds(unsigned char *dst, const uint1
 
 // The register fragments of a tile landed by copy_tile_to_lds, in the layout
 // load_tile gives them (head_dim 64).
-__device__ __forceinline__ void read_tile_from_lds(Tile<64> &t, const unsigned char *src,
+__device__ __forceinline__ void read_tile_from_lds(Tile<bf16_t, 64> &t, const unsigned char *src,
                                                    int blk, int rel, int m16, int g) {
   t.blk = blk;
   t.rel = rel;
@@ -288,12 +324,33 @@ __device__ __forceinline__ void read_tile_from_lds(Tile<64> &t, const unsigned c
   }
 }
 
+// The online-softmax update of one tile: x[i] are the base-2 scores of the
+// lane's tokens 4g + i for head l%16 (-inf where masked; every tile has a
+// live token). Updates (m, l), rescales acc when m moved, and returns the
+// probabilities.
+template <int D>
+__device__ __forceinline__ void softmax_update(DecodeState<D> &st, const float (&x)[4],
+                                               float (&pr)[4]) {
+  float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  mx = max_xor32(max_xor16(mx));
+  const float m_new = fmaxf(st.m, mx);  // finite: every tile has a live token
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+  st.l = st.l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+  st.m = m_new;
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) st.acc[n] *= alpha;
+  }
+}
+
 // With kAppend, row t.sub of the tile (if any) takes the appended token's K
 // and V rows, staged in LDS (new_row: K row then V row), in place of what was
 // read from the cache; the substitution is a per-lane select at compute time,
 // so it never waits on the tile's loads and holds no registers before.
 template <int D, bool kAppend>
-__device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
+__device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<bf16_t, D> &t,
                                              const bf16x8_t *qf, float scale,
                                              int live, int g, int m16,
                                              const uint16_t *new_row) {
@@ -329,19 +386,8 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
   float x[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) x[i] = (4 * g + i < lim) ? r[i] * kLog2e : -INFINITY;
-  float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  mx = max_xor32(max_xor16(mx));
-  const float m_new = fmaxf(st.m, mx);  // finite: every tile has a live token
-  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
   float pr[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
-  st.l = st.l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-  st.m = m_new;
-  if (__any(alpha != 1.f)) {
-#pragma unroll
-    for (int n = 0; n < VC; ++n) st.acc[n] *= alpha;
-  }
+  softmax_update(st, x, pr);
   // Tokens past the context may hold anything (even NaN): zero their V.
   if (lim < 16) {
 #pragma unroll
@@ -359,6 +405,63 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<D> &t,
     const uint32_t hi = __builtin_amdgcn_perm(vword<D>(t.v[3], c), vword<D>(t.v[2], c), sel);
     const s16x4_t va = __builtin_bit_cast(s16x4_t, make_uint2(lo, hi));
     st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, st.acc[n], 0, 0, 0);
+  }
+}
+
+// The FP32 tile, on v_mfma_f32_16x16x4_f32 (FP32 products, FP32 sums) with
+// the accumulator layouts of the bf16 tile, so the softmax and the merges are
+// shared. S^T: step (j, e) takes dims 16j + 4g + e of lane group g from K
+// chunk j (its 16-byte load) and the matching q chunk. O^T: step i takes
+// tokens 4g + i, whose probability is the lane's pr[i]; dim block c takes
+// dims VC*m + c of the V rows (VC = D/16 floats per lane and row), so
+// accumulator c holds O[dim VC*(4g + i) + c][head l%16], as in the bf16
+// tile. Scores are q.k times scale in FP32, as the reference's FP32 matmul
+// and scale give them (kernels/reference/paged_attention.py:246-247).
+template <int D, bool kAppend>
+__device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<float, D> &t,
+                                             const f32x4_t *qf, float scale, int live, int g,
+                                             int m16, const float *new_row) {
+  constexpr int QK = D / 16, VC = D / 16;
+  using VT = typename TileTraits<float, D>::VT;
+  typedef float vf_t __attribute__((ext_vector_type(VC)));
+  if (t.blk < 0) return;  // absent tile or invalid block id: no keys (uniform)
+  const int lim = live - t.rel;  // tokens of this tile inside the context
+  if constexpr (kAppend) {
+    if (t.sub >= 0) {  // uniform
+      const bool k_row = m16 == t.sub;
+#pragma unroll
+      for (int j = 0; j < QK; ++j)
+        t.k[j] = select_vec(k_row, *reinterpret_cast<const uint4 *>(new_row + 16 * j + 4 * g),
+                            t.k[j]);
+      const VT vrow = *reinterpret_cast<const VT *>(new_row + D + VC * m16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t.v[i] = select_vec(4 * g + i == t.sub, vrow, t.v[i]);
+    }
+  }
+  f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < QK; ++j) {
+    const f32x4_t k = __builtin_bit_cast(f32x4_t, t.k[j]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[e], qf[j][e], s, 0, 0, 0);
+  }
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = (4 * g + i < lim) ? (s[i] * scale) * kLog2e : -INFINITY;
+  float pr[4];
+  softmax_update(st, x, pr);
+  // Tokens past the context may hold anything (even NaN): zero their V.
+  if (lim < 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * g + i >= lim) t.v[i] = VT{};
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const vf_t v = __builtin_bit_cast(vf_t, t.v[i]);
+#pragma unroll
+    for (int c = 0; c < VC; ++c)
+      st.acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[c], pr[i], st.acc[c], 0, 0, 0);
   }
 }
 
@@ -478,10 +581,18 @@ __device__ __forceinline__ float unpublish(uint32_t w) { return __uint_as_float(
 // hs * kWaves .. + kWaves - 1 serve KV head kvh_base + hs over the same
 // tiles, so with kH = 2 both halves of every slot row are requested by one
 // workgroup at the same time.
-template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH, bool kRope>
+template <typename T, int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH,
+          bool kRope>
 __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkItem &it,
                                             int kvh_base) {
-  constexpr int QK = D / 32;
+  constexpr bool kF32 = std::is_same<T, float>::value;
+  static_assert(kF32 || std::is_same<T, bf16_t>::value, "bf16 or FP32 elements");
+  static_assert(!kF32 || (!kLds && !kRope), "the LDS tile and the rotary embedding are bf16");
+  using S = typename TileTraits<T, D>::S;  // storage element
+  constexpr int QK = TileTraits<T, D>::kKChunks;
+  constexpr int kSize = static_cast<int>(sizeof(T));
+  constexpr int kE = 16 / kSize;          // elements per 16-byte chunk
+  constexpr int kRowChunks = D / kE;      // 16-byte chunks per K (or V) row of one head
   constexpr int VC = D / 16;
   constexpr int kThreads = 64 * kWaves * kH;
   const int lane = threadIdx.x & 63;
@@ -502,12 +613,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // Block ids are read for every tile position the split could hold, within
   // the table's width.
   const bool head_ok = m16 < p.group;
-  const uint16_t *qrow = static_cast<const uint16_t *>(p.q) + b * p.q_sb +
-                         (int64_t)(kvh * p.group + (head_ok ? m16 : 0)) * p.q_sh;
+  const S *qrow = static_cast<const S *>(p.q) + b * p.q_sb +
+                  (int64_t)(kvh * p.group + (head_ok ? m16 : 0)) * p.q_sh;
   uint4 qraw[QK];
 #pragma unroll
   for (int j = 0; j < QK; ++j)
-    qraw[j] = head_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * j + 8 * g)
+    qraw[j] = head_ok ? *reinterpret_cast<const uint4 *>(qrow + 4 * kE * j + kE * g)
                       : make_uint4(0, 0, 0, 0);
   // Token positions fit in 32 bits here (max_blocks * block_size < 2^31;
   // speculative tile positions stay below 2^32): block index and offset by
@@ -537,14 +648,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   const int last_rel = static_cast<int>(last_pos - t0) & ~15;  // tile of ctx - 1
   const int last_tok = static_cast<int>(last_pos - t0) & 15;   // its row
   const bool new_owner = append_here && w == (last_rel >> 4) % kWaves;  // uniform
-  __shared__ __align__(16) uint16_t new_row_s[kH][2 * D];
+  __shared__ __align__(16) S new_row_s[kH][2 * D];
   const int64_t new_slot = kAppend ? p.new_slots[b] : -1;
-  const bool new_is_v = lane >= D / 8;
-  const int new_off = 8 * (new_is_v ? lane - D / 8 : lane);
+  const bool new_is_v = lane >= kRowChunks;
+  const int new_off = kE * (new_is_v ? lane - kRowChunks : lane);
   uint4 new_chunk = make_uint4(0, 0, 0, 0);
-  if (new_owner && lane < D / 4)
+  if (new_owner && lane < 2 * kRowChunks)
     new_chunk = *reinterpret_cast<const uint4 *>(
-        static_cast<const uint16_t *>(new_is_v ? p.new_v : p.new_k) + b * p.new_sb +
+        static_cast<const S *>(new_is_v ? p.new_v : p.new_k) + b * p.new_sb +
         (int64_t)kvh * p.new_sh + new_off);
   // Fused rotary embedding (p.inv_freq set; fused write only): every wave
   // puts cos and sin of the decode position ctx - 1 for the d/2 frequencies,
@@ -561,10 +672,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 
   const int ntiles = static_cast<int>(ceil_div(t1 - t0, 16));
 
-  // Q^T as the B operand: lane l holds Q[head l%16][32j + 8g .. +8).
-  bf16x8_t qf[QK];
+  // Q^T as the B operand: lane l holds Q[head l%16][4kE j + kE g .. +kE)
+  // (bf16: 32j + 8g; FP32: 16j + 4g), the dims of its K chunks.
+  using QF = typename std::conditional<kF32, f32x4_t, bf16x8_t>::type;
+  QF qf[QK];
 #pragma unroll
-  for (int j = 0; j < QK; ++j) qf[j] = __builtin_bit_cast(bf16x8_t, qraw[j]);
+  for (int j = 0; j < QK; ++j) qf[j] = __builtin_bit_cast(QF, qraw[j]);
   // Rotates the lane's q fragments: fragment j < QK/2 holds dims
   // 32j + 8g + e (e < 8) and fragment j + QK/2 their partners d/2 further, so
   // each pair is in one lane. LDS operations of one wave complete in order,
@@ -572,6 +685,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // (no instruction) keeps the compiler from moving the other lanes' reads
   // above those writes.
   auto rotate_q = [&]() {
+    if constexpr (!kF32) {
     if (lane < D / 2) {
       // sincosf shares one argument reduction between the two; its results
       // are those of cosf and sinf.
@@ -597,10 +711,11 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
           __builtin_bit_cast(bf16x8_t, make_uint4(bf16_pack2(hi[0], hi[1]), bf16_pack2(hi[2], hi[3]),
                                                   bf16_pack2(hi[4], hi[5]), bf16_pack2(hi[6], hi[7])));
     }
+    }
   };
 
-  const uint16_t *kc = static_cast<const uint16_t *>(p.kc);
-  const uint16_t *vc = static_cast<const uint16_t *>(p.vc);
+  const S *kc = static_cast<const S *>(p.kc);
+  const S *vc = static_cast<const S *>(p.vc);
   const float scale = static_cast<float>(p.scale);
 
   DecodeState<D> st;
@@ -624,9 +739,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   const int row_elems = p.hkv * D;  // elements of one slot (token row)
   const int64_t block_elems = p.block_size * row_elems;
   LaneOffsets lo;
-  lo.k = ((m16 * p.hkv + kvh) * D + 8 * g) * 2;
-  lo.v = ((4 * g * p.hkv + kvh) * D + VC * m16) * 2;
-  lo.v_step = row_elems * 2;
+  lo.k = (m16 * p.hkv + kvh) * D * kSize + 16 * g;
+  lo.v = ((4 * g * p.hkv + kvh) * D + VC * m16) * kSize;
+  lo.v_step = row_elems * kSize;
   const int live = static_cast<int>(t1 - t0);
   // The owning wave stores the new K/V rows to slot new_slots[b] and to LDS,
   // and, when that slot is the one position ctx - 1 maps to, uses them in
@@ -663,12 +778,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
                        bf16_pack2(o[6], o[7]));
       }
     }
-    if (lane < D / 4) {
+    if (lane < 2 * kRowChunks) {
       *reinterpret_cast<uint4 *>(new_row_s[hs] + (new_is_v ? D : 0) + new_off) = v;
       const int64_t num_slots = p.num_blocks * p.block_size;
       if (new_slot >= 0 && new_slot < num_slots) {
-        uint16_t *dst = static_cast<uint16_t *>(new_is_v ? p.vc_w : p.kc_w) +
-                        (new_slot * p.hkv + kvh) * D + new_off;
+        S *dst = static_cast<S *>(new_is_v ? p.vc_w : p.kc_w) +
+                 (new_slot * p.hkv + kvh) * D + new_off;
         *reinterpret_cast<uint4 *>(dst) = v;
       }
     }
@@ -677,14 +792,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   };
   // Marks row last_tok of the new token's tile for substitution when the
   // new slot is the one position ctx - 1 maps to.
-  auto mark_new_row = [&](Tile<D> &t) {
+  auto mark_new_row = [&](Tile<T, D> &t) {
     const bool same_slot =
         t.blk >= 0 &&
         new_slot == (int64_t)t.blk * p.block_size + in_block(static_cast<uint32_t>(last_pos));
     if (same_slot) t.sub = last_tok;
   };
 
-  auto issue = [&](Tile<D>(&buf)[kBatch], int kb) {
+  auto issue = [&](Tile<T, D>(&buf)[kBatch], int kb) {
     if ((kb & 63) == 0) load_block_ids(kb);
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -693,8 +808,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       const int rel = 16 * (w + kWaves * k);
       // Byte offset of the tile's first token inside its block.
       const int tile_off =
-          static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel)) * row_elems * 2;
-      load_tile<D>(buf[u], kc, vc, block_elems, tile_off, blk, rel, lo);
+          static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel)) * row_elems * kSize;
+      load_tile<T, D>(buf[u], kc, vc, block_elems, tile_off, blk, rel, lo);
     }
     if (append_here) {
 #pragma unroll
@@ -704,7 +819,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       }
     }
   };
-  auto compute = [&](Tile<D>(&buf)[kBatch]) {
+  auto compute = [&](Tile<T, D>(&buf)[kBatch]) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
       compute_tile<D, kAppend>(st, buf[u], qf, scale, live, g, m16, new_row_s[hs]);
@@ -716,7 +831,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     // Next batch in flight while the current one computes.
     // Batches are issued whether or not they hold tiles (absent tiles read
     // zeros), so the wait before each compute counts only its own batch.
-    Tile<D> bufA[kBatch], bufB[kBatch];
+    Tile<T, D> bufA[kBatch], bufB[kBatch];
     issue(bufA, 0);
     if (rope) rotate_q();
     if (append_here) stage_new_row();
@@ -732,9 +847,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     // fifth in this wave's LDS slot, all issued up front, so that one
     // workgroup keeps 80 KB in flight and the splits of a batch like 64
     // sequences of up to 4K tokens fit the GPU in one generation.
-    static_assert(D == 64 && kBatch == 4, "LDS landing is laid out for head_dim 64");
+    static_assert(D == 64 && kBatch == 4 && !kF32, "LDS landing is laid out for bf16 head_dim 64");
     __shared__ __align__(16) unsigned char lds_tiles[kWaves * kH][kLdsTileBytes];
-    Tile<D> buf[kBatch];
+    Tile<T, D> buf[kBatch];
     issue(buf, 0);
     const int rel4 = 16 * (w + kWaves * kBatch);
     const int blk4 = kBatch < nk ? __builtin_amdgcn_readlane(blk_reg, kBatch) : -1;
@@ -752,7 +867,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   } else {
     // Issued whatever nk is (absent tiles read zeros), so that every path
     // reaching the computes has the same loads in flight.
-    Tile<D> buf[kBatch];
+    Tile<T, D> buf[kBatch];
     issue(buf, 0);
     if (rope) rotate_q();
     if (append_here) stage_new_row();
@@ -789,7 +904,11 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // (t + kThreads r) % D).
   const int ngh = kH * p.group;
   const int head0 = kvh_base * p.group;
-  uint16_t *out = static_cast<uint16_t *>(p.out);
+  S *out = static_cast<S *>(p.out);
+  auto store_out = [&](float x) -> S {
+    if constexpr (kF32) return x;
+    else return float_to_bf16_bits(x);
+  };
   // The workgroup's partial rows: (m, l) pairs and acc rows for its heads h
   // and splits s at row h * split_stride + s, under buffer resources of their
   // span (at most 16 heads x 8192 splits x 128 dims of FP32: 32-bit offsets).
@@ -826,7 +945,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         den += f * l_s[w0 + ww][hg];
       }
       if (nsplits == 1) {
-        out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num / den);
+        out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = store_out(num / den);
       } else if (merger) {
         own[r] = num;
         if (d == 0) {
@@ -1022,7 +1141,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     for (int r = 0; r < kMaxOut; ++r) {
       const int idx = threadIdx.x + kThreads * r;
       if (idx < nout)
-        out[b * p.o_sb + (int64_t)(head0 + idx / D) * p.o_sh + idx % D] = 0x7FC0u;  // bf16 NaN
+        out[b * p.o_sb + (int64_t)(head0 + idx / D) * p.o_sh + idx % D] = store_out(__builtin_nanf(""));
     }
     return;
   }
@@ -1031,7 +1150,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     const int idx = threadIdx.x + kThreads * r;
     if (idx < nout) {
       const int h = idx / D, d = idx % D;
-      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = float_to_bf16_bits(num[r] / den_s[h]);
+      out[b * p.o_sb + (int64_t)(head0 + h) * p.o_sh + d] = store_out(num[r] / den_s[h]);
     }
   }
 }
@@ -1040,43 +1159,47 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 // (sequence, split) are adjacent workgroups; the grid is sized for the widest
 // table and the workgroups past the live items exit after the context
 // lengths.
-template <int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH, bool kRope>
+template <typename T, int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH,
+          bool kRope>
 __global__ __launch_bounds__(64 * kWaves * kH) void decode_mfma(DecodeParams p) {
   const int64_t cap = p.max_blocks * p.block_size;
   const int nhg = p.hkv / kH;  // KV-head groups per item
   const WorkItem it = find_item(p, blockIdx.x / nhg, cap);
   if (it.b < 0) return;  // uniform
-  decode_item<D, kBatch, kDouble, kAppend, kLds, kH, kRope>(p, it, (blockIdx.x % nhg) * kH);
+  decode_item<T, D, kBatch, kDouble, kAppend, kLds, kH, kRope>(p, it, (blockIdx.x % nhg) * kH);
 }
 
 }  // namespace
 
 bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
                           int64_t block_size) {
-  return dtype == MLR_DTYPE_BF16 && (head_dim == 64 || head_dim == 128) &&
-         group >= 1 && group <= 16 && block_size % 16 == 0;
+  return (dtype == MLR_DTYPE_BF16 || dtype == MLR_DTYPE_F32) &&
+         (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 16 &&
+         block_size % 16 == 0;
 }
 
-template <int D, int B, bool DB, bool A, bool L, int H, bool R>
+template <typename T, int D, int B, bool DB, bool A, bool L, int H, bool R>
 int launch_one(const DecodeParams &p, hipStream_t stream) {
   // Every (sequence, split) item that can exist, times the KV-head groups.
   const int64_t items = (int64_t)p.batch * p.max_splits * (p.hkv / H);
   if (items > 0x7fffffff)
     return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_decode: %lld work items exceed the grid",
                      (long long)items);
-  decode_mfma<D, B, DB, A, L, H, R><<<dim3(static_cast<unsigned>(items)), 64 * kWaves * H, 0,
-                                      stream>>>(p);
+  decode_mfma<T, D, B, DB, A, L, H, R><<<dim3(static_cast<unsigned>(items)), 64 * kWaves * H,
+                                         0, stream>>>(p);
   return check_launch("mlr_paged_decode(mfma)");
 }
 
 // The three variants of one layout: decode only, with the fused KV write,
 // and with the fused write and rotary embedding (their own instantiations,
-// so the rotary code costs the other two nothing).
-template <int D, int B, bool DB, bool L, int H = 1>
+// so the rotary code costs the other two nothing; bf16 only).
+template <typename T, int D, int B, bool DB, bool L, int H = 1>
 int launch_variant(const DecodeParams &p, hipStream_t stream) {
-  if (p.new_k == nullptr) return launch_one<D, B, DB, false, L, H, false>(p, stream);
-  if (p.inv_freq == nullptr) return launch_one<D, B, DB, true, L, H, false>(p, stream);
-  return launch_one<D, B, DB, true, L, H, true>(p, stream);
+  if (p.new_k == nullptr) return launch_one<T, D, B, DB, false, L, H, false>(p, stream);
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    if (p.inv_freq != nullptr) return launch_one<T, D, B, DB, true, L, H, true>(p, stream);
+  }
+  return launch_one<T, D, B, DB, true, L, H, false>(p, stream);
 }
 
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
@@ -1094,22 +1217,35 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
   const int cus = current_device_cus();
   const bool pairs = p.hkv % 2 == 0 && 2 * p.group <= 16 && cus > 0 &&
                      (int64_t)p.batch * p.max_splits * (p.hkv / 2) >= cus;
-  // Instantiations: head_dim x (one load batch | + LDS tile | double-buffered)
-  // x KV heads per workgroup x variant.
-  if (p.d == 64) {
-    if (tiles_per_wave <= 4) return launch_variant<64, 4, false, false>(p, stream);
-    if (p.ts == kLdsSplit64) {
-      if (pairs) return launch_variant<64, 4, false, true, 2>(p, stream);
-      return launch_variant<64, 4, false, true>(p, stream);
+  // FP32: a tile takes twice the registers of a bf16 one. At head_dim 64 up to
+  // four tiles per wave go in one batch (batch 4 x {17, 64, 130, 255} tokens,
+  // 14/2 heads: 8.42 us per step against 8.57 us in two double-buffered
+  // batches of two), longer splits in double-buffered batches of two; at
+  // head_dim 128 one tile per batch. One KV head per workgroup.
+  if (p.dtype == MLR_DTYPE_F32) {
+    if (p.d == 64) {
+      if (tiles_per_wave <= 4) return launch_variant<float, 64, 4, false, false>(p, stream);
+      return launch_variant<float, 64, 2, true, false>(p, stream);
     }
-    return launch_variant<64, 4, true, false>(p, stream);
+    if (tiles_per_wave <= 1) return launch_variant<float, 128, 1, false, false>(p, stream);
+    return launch_variant<float, 128, 1, true, false>(p, stream);
+  }
+  // bf16 instantiations: head_dim x (one load batch | + LDS tile |
+  // double-buffered) x KV heads per workgroup x variant.
+  if (p.d == 64) {
+    if (tiles_per_wave <= 4) return launch_variant<bf16_t, 64, 4, false, false>(p, stream);
+    if (p.ts == kLdsSplit64) {
+      if (pairs) return launch_variant<bf16_t, 64, 4, false, true, 2>(p, stream);
+      return launch_variant<bf16_t, 64, 4, false, true>(p, stream);
+    }
+    return launch_variant<bf16_t, 64, 4, true, false>(p, stream);
   }
   if (pairs) {
-    if (tiles_per_wave <= 2) return launch_variant<128, 2, false, false, 2>(p, stream);
-    return launch_variant<128, 2, true, false, 2>(p, stream);
+    if (tiles_per_wave <= 2) return launch_variant<bf16_t, 128, 2, false, false, 2>(p, stream);
+    return launch_variant<bf16_t, 128, 2, true, false, 2>(p, stream);
   }
-  if (tiles_per_wave <= 2) return launch_variant<128, 2, false, false>(p, stream);
-  return launch_variant<128, 2, true, false>(p, stream);
+  if (tiles_per_wave <= 2) return launch_variant<bf16_t, 128, 2, false, false>(p, stream);
+  return launch_variant<bf16_t, 128, 2, true, false>(p, stream);
 }
 
 }  // namespace mlr

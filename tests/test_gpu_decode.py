@@ -89,7 +89,10 @@ CASES = [
     (torch.bfloat16, 40, 2, 64, 16, [77]),                         # generic (G=20)
     (torch.bfloat16, 8, 2, 96, 16, [50, 200]),                     # generic (D=96)
     (torch.float16, 14, 2, 64, 16, [31, 257]),
-    (torch.float32, 14, 2, 64, 16, [1, 255, 600]),
+    (torch.float32, 14, 2, 64, 16, [1, 255, 600]),                 # FP32 MFMA, merged splits
+    (torch.float32, 28, 4, 128, 16, [33, 700, 2049]),              # FP32 MFMA, D=128
+    (torch.float32, 32, 2, 64, 32, [64, 513, 1]),                  # FP32 MFMA, G=16, BS=32
+    (torch.float32, 14, 2, 64, 8, [9, 130]),                       # generic (BS=8)
     (torch.float32, 6, 3, 40, 5, [7, 23]),
     (torch.float64, 4, 2, 16, 4, [3, 19]),
 ]
@@ -123,7 +126,8 @@ def test_split_size_does_not_change_the_result(device, tokens_per_split):
     (torch.bfloat16, [1, 16, 17, 300, 1000, 257], 0),     # fused in the MFMA kernel
     (torch.bfloat16, [33, 64, 500], 64),
     (torch.bfloat16, [300, 384, 770, 5], 384),              # new token in an LDS tile
-    (torch.float32, [5, 255, 256], 0),                     # write kernel, then decode
+    (torch.float32, [5, 255, 256], 0),                     # fused in the FP32 MFMA kernel
+    (torch.float32, [300, 384, 770, 5, 1000, 2049], 64),   # FP32, splits merged in-launch
 ])
 def test_decode_append_equals_write_then_decode(device, dtype, lens, tokens_per_split):
     """mlr_paged_decode_append: same cache bits and same output bits as
