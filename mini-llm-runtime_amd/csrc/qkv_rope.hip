@@ -65,7 +65,8 @@ struct alignas(VEC * sizeof(T)) Vec {
   T v[VEC];
 };
 
-// One wave per token (grid-stride over tokens). A token's row is cut into
+// One wave per token (grid-stride over tokens; a workgroup holds one wave,
+// or four for large launches). A token's row is cut into
 // chunks of VEC elements: a rotary chunk is VEC elements of the first half of
 // a q or k head with their partners in the second half; a v chunk is VEC
 // elements of a v head. A lane takes K chunks per pass. The position and the
@@ -74,7 +75,7 @@ struct alignas(VEC * sizeof(T)) Vec {
 // together and the cos/sin table is built under their latency; only the
 // stores depend on the chunk kind.
 template <typename T, typename I, int VEC, int K>
-__global__ __launch_bounds__(64) void qkv_rope_write_kernel(
+__global__ __launch_bounds__(256) void qkv_rope_write_kernel(
     const T *__restrict__ qkv, int64_t qkv_st, const T *__restrict__ bias,
     const int64_t *__restrict__ positions, const float *__restrict__ inv_freq,
     const void *__restrict__ slots, T *__restrict__ q_out, int64_t q_st,
@@ -82,15 +83,22 @@ __global__ __launch_bounds__(64) void qkv_rope_write_kernel(
     int hkv, int d) {
 #pragma clang fp contract(off)
   using V = Vec<T, VEC>;
-  extern __shared__ float cs[];  // [d/2] cos then [d/2] sin, dtype-rounded
-  const int lane = threadIdx.x;
+  // Per wave: [d/2] cos then [d/2] sin, dtype-rounded. The wave's own rows:
+  // LDS operations of one wave complete in order, and the wave barriers
+  // (no instruction) keep the compiler from reordering across them.
+  extern __shared__ float cs_all[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  float *cs = cs_all + wv * d;
   const int half = d / 2;
   const int cph = half / VEC;  // rotary chunks per head
   const int n_rope = (hq + hkv) * cph;
   const int n_chunks = n_rope + hkv * d / VEC;
   const int v_base = (hq + hkv) * d;
   const float my_freq = lane < half ? inv_freq[lane] : 0.f;
-  for (int64_t t = blockIdx.x; t < num_tokens; t += gridDim.x) {
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * waves + wv; t < num_tokens;
+       t += static_cast<int64_t>(gridDim.x) * waves) {
     const T *row = qkv + t * qkv_st;
     const float pos = static_cast<float>(positions[t]);
     const int64_t slot = load_index<I>(slots, t);
@@ -123,7 +131,7 @@ __global__ __launch_bounds__(64) void qkv_rope_write_kernel(
           cs[i] = cv;
           cs[half + i] = sv;
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
       }
 #pragma unroll
       for (int k = 0; k < K; ++k) {
@@ -165,7 +173,7 @@ __global__ __launch_bounds__(64) void qkv_rope_write_kernel(
         }
       }
     }
-    __syncthreads();  // cs is rewritten for the next token
+    __builtin_amdgcn_wave_barrier();  // cs is rewritten for the next token
   }
 }
 
@@ -174,9 +182,15 @@ void launch_vec(const void *qkv, int64_t qkv_st, const void *bias, const int64_t
                 const float *inv_freq, const void *slots, void *q_out, int64_t q_st, void *kc,
                 void *vc, int64_t num_slots, int64_t num_tokens, int hq, int hkv, int d,
                 hipStream_t stream) {
-  const int64_t blocks = num_tokens < 65536 ? num_tokens : 65536;
-  const size_t lds = static_cast<size_t>(d) * sizeof(float);
-  qkv_rope_write_kernel<T, I, VEC, 4><<<static_cast<unsigned>(blocks), 64, lds, stream>>>(
+  // Four tokens (waves) per workgroup from 1024 tokens on, one below it.
+  // Measured at a Qwen2.5-0.5B layer, bf16, in 100-call graphs: 2048
+  // tokens 4.39 us against 4.53 us with one wave per workgroup (eight per
+  // workgroup: 4.40 us); 48 tokens 3.30 us against 3.18 us.
+  const int waves = num_tokens >= 1024 ? 4 : 1;
+  const int64_t wgs = (num_tokens + waves - 1) / waves;
+  const int64_t blocks = wgs < 65536 ? wgs : 65536;
+  const size_t lds = static_cast<size_t>(waves) * d * sizeof(float);
+  qkv_rope_write_kernel<T, I, VEC, 4><<<static_cast<unsigned>(blocks), 64 * waves, lds, stream>>>(
       static_cast<const T *>(qkv), qkv_st, static_cast<const T *>(bias), positions, inv_freq,
       slots, static_cast<T *>(q_out), q_st, static_cast<T *>(kc), static_cast<T *>(vc),
       num_slots, num_tokens, hq, hkv, d);

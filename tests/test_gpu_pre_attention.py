@@ -60,13 +60,15 @@ def split_heads(x, hq, hkv, d):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-@pytest.mark.parametrize("tokens", [1, 37, 300])
+# 1030 and 2048 tokens take four tokens per workgroup (1030: a partial last one).
+@pytest.mark.parametrize("tokens", [1, 37, 300, 1030, 2048])
 @pytest.mark.parametrize("with_bias", [False, True], ids=["nobias", "bias"])
 def test_bit_exact_against_unfused_torch_path(device, dtype, shape, tokens, with_bias):
     hq, hkv, d = shape
     index_dtype = torch.int32 if tokens % 2 else torch.int64
     qkv, bias, positions, slots, pool = make_case(tokens + d, tokens, hq, hkv, d, dtype,
-                                                  with_bias, index_dtype)
+                                                  with_bias, index_dtype,
+                                                  num_blocks=max(40, tokens // 16 + 8))
     rot = Qwen2RotaryEmbedding(d, THETA).to(device)
     qkv_d, pos_d, slots_d = qkv.to(device), positions.to(device), slots.to(device)
     bias_d = bias.to(device) if bias is not None else None
