@@ -88,6 +88,12 @@ def parse_args():
                    help="time only the end-to-end serving steps (qwen05b_serving, BF16)")
     p.add_argument("--no-serving", action="store_true",
                    help="leave the serving steps out of the default run")
+    p.add_argument("--no-contiguous", action="store_true",
+                   help="leave out the contiguous-placement comparators of the decode step "
+                        "(they launch the step's own kernel, which a kernel trace would "
+                        "then lump with it)")
+    p.add_argument("--contiguous-only", action="store_true",
+                   help="with --profile: launch only the contiguous-placement comparators")
     return p.parse_args()
 
 
@@ -173,6 +179,28 @@ def sample_sclk(replay, seconds=1.5):
                       "the workload's graph replays untimed"}
 
 
+def contiguous_tables(wl, device):
+    """Contiguous placements of a decode workload's K/V rows (the reference
+    times dense attention on contiguous K/V beside its paged decode): the same
+    context lengths with each sequence's blocks consecutive in the pool
+    (bt_seq, with the new token's slots slots_seq), and the same token rows as
+    one run of consecutive blocks (bt_flat, one sequence of ctx_flat tokens)."""
+    import torch
+
+    need = [-(-int(n) // 16) for n in wl.context_lens.tolist()]
+    batch = len(need)
+    starts = [sum(need[:b]) for b in range(batch)]
+    bt_seq = torch.full_like(wl.block_tables, -1)
+    for b, (s0, n) in enumerate(zip(starts, need)):
+        bt_seq[b, :n] = torch.arange(s0, s0 + n)
+    slots_seq = torch.tensor([int(bt_seq[b, (n - 1) // 16]) * 16 + (n - 1) % 16
+                              for b, n in enumerate(wl.context_lens.tolist())])
+    total_tokens = int(wl.context_lens.sum())
+    bt_flat = torch.arange(-(-total_tokens // 16)).unsqueeze(0)
+    ctx_flat = torch.tensor([total_tokens])
+    return tuple(t.to(device) for t in (bt_seq, slots_seq, bt_flat, ctx_flat))
+
+
 def profile_run(args, device):
     """Eager, untimed launches of the benchmarked kernels (for rocprofv3)."""
     import torch
@@ -192,6 +220,29 @@ def profile_run(args, device):
     out = torch.empty_like(q)
     ws = torch.zeros(kpa.decode_workspace_bytes(64, 14, 64, bt.shape[1] * 16, torch.bfloat16),
                      dtype=torch.uint8, device=device)
+    if args.contiguous_only:
+        # The decode step on per-sequence contiguous blocks, the read floor
+        # on those tables, and the read floor over the same rows as one run.
+        bt_seq, slots_seq, bt_flat, ctx_flat = contiguous_tables(wl, device)
+        seq_out = torch.empty(64 * -(-bt.shape[1] * 16 // 96), dtype=torch.int32, device=device)
+        flat_out = torch.empty(-(-bt_flat.shape[1] * 16 // 96), dtype=torch.int32,
+                               device=device)
+        for i in range(args.steps):
+            k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
+            kpa.paged_decode_launch(q, k_layer, v_layer, bt_seq, ctx, out, workspace=ws,
+                                    new_k=new_k, new_v=new_v, slot_mapping=slots_seq)
+        for i in range(args.steps):
+            k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
+            kpa.paged_kv_read_floor(k_layer, v_layer, bt_seq, ctx, tokens_per_item=96,
+                                    out=seq_out)
+        for i in range(args.steps):
+            k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
+            kpa.paged_kv_read_floor(k_layer, v_layer, bt_flat, ctx_flat, tokens_per_item=96,
+                                    out=flat_out)
+        torch.cuda.synchronize()
+        print(f"profile: {args.steps} each of the contiguous-block step, the contiguous-block "
+              "read floor and the one-run read floor", flush=True)
+        return
     for i in range(args.steps):
         k_layer, v_layer = cache.get_layer_cache(i % LAYERS)
         kpa.paged_decode_launch(q, k_layer, v_layer, bt, ctx, out, workspace=ws, new_k=new_k,
@@ -211,13 +262,13 @@ def profile_run(args, device):
     for i in range(LAYERS):
         kpre.qkv_rope_decode(qkv, inv_freq, cache, i % LAYERS, slots, bt, ctx, 14, out=out,
                              workspace=ws)
-    floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // 320), dtype=torch.int32, device=device)
+    floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // 96), dtype=torch.int32, device=device)
     for i in range(LAYERS):
         k_layer, v_layer = cache.get_layer_cache(i)
-        kpa.paged_kv_read_floor(k_layer, v_layer, bt, ctx, tokens_per_item=320, out=floor_out)
+        kpa.paged_kv_read_floor(k_layer, v_layer, bt, ctx, tokens_per_item=96, out=floor_out)
     torch.cuda.synchronize()
     print(f"profile: {args.steps} decode steps, {LAYERS} decode-only steps, {LAYERS} one-launch "
-          f"served steps, {LAYERS} read-floor passes", flush=True)
+          f"served steps, {LAYERS} read-floor passes (96-token items)", flush=True)
     del cache
     if not args.no_prefill:
         pw = workloads.bf16_prefill_chunk512_x8()
@@ -269,6 +320,19 @@ def profile_run(args, device):
     torch.cuda.synchronize()
     print(f"profile: 12 decode calls of {lw.name} over {POOLS_32K} pools", flush=True)
     del pools
+    # The FP32 batch-4 decode step (write folded in, one launch).
+    fw = workloads.fp32_decode_b4()
+    fkc, fvc = fw.k_cache.to(device), fw.v_cache.to(device)
+    fq, fbt, fctx = fw.q.to(device), fw.block_tables.to(device), fw.context_lens.to(device)
+    fslots, fnk, fnv = (t.to(device) for t in (fw.slot_mapping, fw.new_k, fw.new_v))
+    fout = torch.empty_like(fq)
+    fws = torch.zeros(kpa.decode_workspace_bytes(4, 14, 64, fbt.shape[1] * 16, torch.float32),
+                      dtype=torch.uint8, device=device)
+    for _ in range(20):
+        kpa.paged_decode_launch(fq, fkc, fvc, fbt, fctx, fout, workspace=fws, new_k=fnk,
+                                new_v=fnv, slot_mapping=fslots)
+    torch.cuda.synchronize()
+    print(f"profile: 20 {fw.name} steps", flush=True)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -328,21 +392,8 @@ def bench_decode(args, device):
     floor_items = (64, 96, 160, 320)
     floor_out = torch.empty(64 * -(-bt.shape[1] * 16 // min(floor_items)), dtype=torch.int32,
                             device=device)
-    # Contiguous comparators (the reference times dense attention on
-    # contiguous K/V beside its paged decode): the same context lengths with
-    # each sequence's blocks consecutive in the pool (bt_seq), and the same
-    # token rows as one run of consecutive blocks (bt_flat, one sequence).
-    need = [-(-int(n) // 16) for n in wl.context_lens.tolist()]
-    starts = [sum(need[:b]) for b in range(64)]
-    bt_seq = torch.full_like(wl.block_tables, -1)
-    for b, (s0, n) in enumerate(zip(starts, need)):
-        bt_seq[b, :n] = torch.arange(s0, s0 + n)
-    slots_seq = torch.tensor([int(bt_seq[b, (n - 1) // 16]) * 16 + (n - 1) % 16
-                              for b, n in enumerate(wl.context_lens.tolist())])
-    total_tokens = int(wl.context_lens.sum())
-    bt_flat = torch.arange(-(-total_tokens // 16)).unsqueeze(0)
-    bt_seq, slots_seq, bt_flat = (t.to(device) for t in (bt_seq, slots_seq, bt_flat))
-    ctx_flat = torch.tensor([total_tokens], device=device)
+    # Contiguous comparators of the same step and rows.
+    bt_seq, slots_seq, bt_flat, ctx_flat = contiguous_tables(wl, device)
     flat_out = torch.empty(-(-bt_flat.shape[1] * 16 // 96), dtype=torch.int32, device=device)
 
     def step(layer, kind="step"):
@@ -401,8 +452,9 @@ def bench_decode(args, device):
     t_step = timed_graph(g_steps, 1, stream)
     # A larger sample of the same graph (10 replays) as a cross-check.
     t_step10 = timed_graph(g_steps, 10, stream) / 10
+    contiguous = () if args.no_contiguous else ("contig", "floor_seq", "floor_flat")
     graphs = {kind: capture(kind, LAYERS)
-              for kind in ("decode", "served", "served1", "contig", "floor_seq", "floor_flat",
+              for kind in ("decode", "served", "served1", *contiguous,
                            *(f"floor{n}" for n in floor_items))}
     res = {}
     for kind, g in graphs.items():
@@ -428,7 +480,7 @@ def bench_decode(args, device):
         "GBps": round(kv_bytes / (floor_us[best] * 1e-6) / 1e9, 1),
         "frac_of_hbm_peak": round(kv_bytes / (floor_us[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "step_us_over_floor_us": round(sec_per_step * 1e6 / floor_us[best], 3),
-        "contiguous": {
+        "contiguous": None if args.no_contiguous else {
             "what": "the same step and the same K/V rows with contiguous placement: "
                     "step_us = mlr_paged_decode_append with each sequence's blocks consecutive "
                     "in the pool; floor_seq_us = the read floor on those tables (96-token "
@@ -915,15 +967,38 @@ def bench_serving(device, steps=None):
     }
 
 
+def kernel_sources_hash():
+    """sha256 (first 16 hex digits) over the kernel sources and the ABI header:
+    what a counter profile of the kernels depends on."""
+    import glob
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(REPO, "mini-llm-runtime_amd", "csrc", "*")) +
+                   glob.glob(os.path.join(REPO, "include", "*.h")))
+    for path in files:
+        h.update(os.path.relpath(path, REPO).encode())
+        with open(path, "rb") as f:
+            h.update(hashlib.sha256(f.read()).digest())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary (profiles/traffic.json), or None when it is absent."""
+    summary (profiles/traffic.json), measured outside this run (counters need
+    their own rocprofv3 passes). Used only when it was measured on these kernel
+    sources: the file records their hash, and a profile of other sources is
+    stale, so the line then carries traffic null and says why."""
     path = os.path.join(REPO, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)
+            traffic = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, "profiles/traffic.json is absent"
+    if traffic.get("kernel_sources_sha256_16") != kernel_sources_hash():
+        return None, ("profiles/traffic.json was measured on other kernel sources "
+                      f"({traffic.get('kernel_sources_sha256_16')}; now {kernel_sources_hash()})")
+    return traffic, traffic["source"]
 
 
 def provenance():
@@ -996,7 +1071,7 @@ def main():
         cpu = cpu_baseline_decode(dec["wl"], args.cpu_budget)
         if pre is not None:
             cpu_pre = cpu_baseline_prefill(pre["wl"], args.cpu_budget / 2)
-    traffic = measured_traffic()
+    traffic, traffic_source = measured_traffic()
     line = {
         "metric": METRIC,
         "value": round(dec["value_gbs"], 2),
@@ -1041,7 +1116,7 @@ def main():
             "unit": "GB/s",
             "frac": round(dec["value_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic["decode_step_bytes"] if traffic else None,
-            "traffic_source": traffic["source"] if traffic else None,
+            "traffic_source": traffic_source,
             "algorithmic_bytes_per_launch": dec["step_bytes"],
             "avg_launch_us": round(dec["ms_per_step"] * 1e3, 3),
         },
@@ -1056,13 +1131,16 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 3),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 5),
-                         "traffic": traffic["prefill_call_bytes"] if traffic else None},
+                         "traffic": traffic["prefill_call_bytes"] if traffic else None,
+                         "traffic_source": traffic_source},
             "flops_per_call": pre["flops_per_call"],
             "us_per_call": pre["us_per_call"],
             "us_per_call_min_max": pre["us_per_call_min_max"],
             "kv_tile": ("the call passes the reference's tile_size 64, which orders the FP32 "
                         "accumulation only; the kernel steps by its own 64-key tile for "
-                        "any tile_size, so there is one timing, not a tile sweep"),
+                        "any tile_size, so there is one timing, not a tile sweep (a "
+                        "128-key instantiation, one workgroup per CU, measured 89.5 us "
+                        "against 53.6 us on one box and was not kept)"),
             "sclk_mhz": pre["sclk"],
             "cpu_baseline": cpu_pre,
         }
