@@ -154,14 +154,15 @@ def test_decode_append_equals_write_then_decode(device, dtype, lens, tokens_per_
     assert max_abs(fused, want) <= TOL[dtype]
 
 
-def _fused_and_plain_vs_oracle(device, lens, hq, hkv, d, tokens_per_split, seed):
+def _fused_and_plain_vs_oracle(device, lens, hq, hkv, d, tokens_per_split, seed,
+                               dtype=torch.bfloat16):
     """The fused write against write-then-decode (same cache bits, same output
-    bits) and the decode against the oracle, BF16."""
-    q, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, 16, dtype=torch.bfloat16,
+    bits) and the decode against the oracle."""
+    q, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, 16, dtype=dtype,
                                              seed=seed, fill=0.0)
     gen = torch.Generator().manual_seed(seed + 1)
-    new_k = torch.randn(len(lens), hkv, d, generator=gen).bfloat16()
-    new_v = torch.randn(len(lens), hkv, d, generator=gen).bfloat16()
+    new_k = torch.randn(len(lens), hkv, d, generator=gen).to(dtype)
+    new_v = torch.randn(len(lens), hkv, d, generator=gen).to(dtype)
     slots = torch.tensor([tables[b][(n - 1) // 16] * 16 + (n - 1) % 16
                           for b, n in enumerate(lens)])
     q, bt, sl, slots_d = (t.to(device) for t in (q, bt, sl, slots))
@@ -177,7 +178,32 @@ def _fused_and_plain_vs_oracle(device, lens, hq, hkv, d, tokens_per_split, seed)
     assert torch.equal(fused, plain)
     want = opa.decode_batch_loop(q.cpu(), k2.cpu(), v2.cpu(), tables, lens, 16)
     assert torch.isfinite(plain).all()
-    assert max_abs(plain, want) <= 2e-2
+    assert max_abs(plain, want) <= TOL[dtype]
+
+
+# Every FP32 instantiation the launcher picks (tiles per wave =
+# ceil(tokens_per_split / 64)): head_dim 64 with up to four tiles in one load
+# batch, or double-buffered batches of two; head_dim 128 with one tile, or
+# double-buffered single tiles. GQA groups 7, 1 and 8; contexts from one token
+# to 4000 (up to 63 splits merged in the launch).
+FP32_LENS = [4000, 1, 17, 64, 65, 255, 256, 257, 640, 1500, 2049, 3333]
+
+
+@pytest.mark.parametrize("d,hq,hkv,tokens_per_split", [
+    (64, 14, 2, 64),     # one tile per wave
+    (64, 14, 2, 256),    # four tiles in one batch (the fp32_decode_b4 layout)
+    (64, 14, 2, 512),    # double-buffered batches of two
+    (64, 8, 8, 272),     # GQA group 1, double-buffered
+    (64, 16, 2, 0),      # GQA group 8, default split
+    (128, 28, 4, 64),    # head_dim 128, one tile
+    (128, 28, 4, 256),   # head_dim 128, double-buffered
+    (128, 16, 2, 0),     # head_dim 128, GQA group 8, default split
+], ids=lambda v: str(v))
+def test_fp32_every_layout_matches_oracle(device, d, hq, hkv, tokens_per_split):
+    """FP32 on the matrix-core kernel: the fused write equals write-then-decode
+    bit for bit, and the decode is within 1e-5 of the oracle."""
+    _fused_and_plain_vs_oracle(device, FP32_LENS, hq, hkv, d, tokens_per_split, seed=61 + d,
+                               dtype=torch.float32)
 
 
 # Enough (sequence, split) items that the launcher gives every workgroup a
@@ -473,16 +499,17 @@ def test_workspace_survives_calls_of_other_shapes(device):
         assert int(torch.count_nonzero(ws)) == 0, i
 
 
-def test_merge_distrusts_a_flagged_workspace(device):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_merge_distrusts_a_flagged_workspace(device, dtype):
     """The workspace's first word is what a merge that waited past its limit
     leaves behind (set here from the host; every kernel exits normally).
     Such a workspace is not trusted: every sequence whose splits are merged
     gets NaN, and sequences that fit one split are still exact."""
     lens = [100, 1000, 3000, 320, 321, 17]
     ts = 320
-    q, kc, vc, bt, sl, tables = random_paged(lens, 14, 2, 64, 16, dtype=torch.bfloat16, seed=5)
+    q, kc, vc, bt, sl, tables = random_paged(lens, 14, 2, 64, 16, dtype=dtype, seed=5)
     ws = torch.zeros(kpa.decode_workspace_bytes(len(lens), 14, 64, bt.shape[1] * 16,
-                                                torch.bfloat16, ts),
+                                                dtype, ts),
                      dtype=torch.uint8, device=device)
     ws[:4].view(torch.int32).fill_(1)
     got = kpa.paged_decode_launch(q.to(device), kc.to(device), vc.to(device), bt.to(device),
@@ -491,7 +518,7 @@ def test_merge_distrusts_a_flagged_workspace(device):
     got = got.float().cpu()
     for i, n in enumerate(lens):
         if n <= ts:
-            assert max_abs(got[i], want[i]) <= 2e-2, i
+            assert max_abs(got[i], want[i]) <= TOL[dtype], i
         else:
             assert torch.isnan(got[i]).all(), i
 

@@ -3,8 +3,9 @@ scratch, for callers that cannot allocate) against mlr_paged_decode_append
 with a caller workspace, through the C ABI.
 
 The two entry points run the same kernels, so outputs and the K/V written to
-the cache must be identical bit for bit. Two calls in a row, the second with a
-smaller batch (the scratch keeps the first call's contents), then an oversized
+the cache must be identical bit for bit. Calls in a row, each later one with a
+smaller batch (the scratch keeps the earlier calls' contents; the last ones in
+FP32), then an oversized
 request that must be rejected before anything is launched or written. The
 call is also captured into a graph (where allocation is refused) and its
 replays compared with the workspace entry point, and the scratch's
@@ -80,6 +81,14 @@ def test_static_scratch_decode_equals_workspace_decode(device):
     slots = torch.tensor([tables[b][(n - 1) // 16] * 16 + (n - 1) % 16
                           for b, n in enumerate(lens)])
     args = [t.to(device) for t in (q, kc, vc, bt, sl, new_k, new_v, slots)]
+    _check_pair(device, *args)
+    _check_pair(device, *args, tokens_per_split=64)
+
+    # Call 3, FP32: the batch-4 step (one split per sequence), then with
+    # 64-token splits merged in the launch.
+    wl = workloads.fp32_decode_b4()
+    args = [t.to(device) for t in (wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
+                                   wl.context_lens, wl.new_k, wl.new_v, wl.slot_mapping)]
     _check_pair(device, *args)
     _check_pair(device, *args, tokens_per_split=64)
 
