@@ -650,6 +650,56 @@ def bench_pre_attention(device, reps=4, calls_per_graph=100):
     }
 
 
+def bench_kv_write(device, reps=4, calls_per_graph=100):
+    """PagedKVCache.write_slots on its own (mlr_kv_write, BF16 into a BF16 layer
+    pool of 24,576 blocks x 16 slots, Qwen2.5-0.5B KV heads): 64 tokens, the
+    decode step's write, and 4096 tokens, the eight 512-token chunks of the
+    chunk-prefill workload; distinct random slots. Timed like the
+    pre-attention leg (graphs of `calls_per_graph` calls), with the graph
+    node's own cost (a one-element fill) beside it. Algorithmic bytes per
+    call: 2 T Hkv D (2 + 2) + 8 T (K and V read and written, int64 slots)."""
+    import torch
+
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+
+    hkv, d = 2, 64
+    cache = PagedKVCache(1, 24576, 16, hkv, d, dtype=torch.bfloat16, device=device)
+    stream = torch.cuda.Stream(device)
+
+    def graph_us(fn):
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(calls_per_graph):
+                fn()
+        warm_graph(g, stream, seconds=0.25)
+        return timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
+
+    node = torch.zeros(1, device=device)
+    node_us = graph_us(lambda: node.zero_())
+    out = {}
+    for tokens in (64, 4096):
+        gen = torch.Generator().manual_seed(tokens)
+        k = torch.randn(tokens, hkv, d, generator=gen).to(torch.bfloat16).to(device)
+        v = torch.randn(tokens, hkv, d, generator=gen).to(torch.bfloat16).to(device)
+        slots = torch.randperm(cache.num_blocks * 16, generator=gen)[:tokens].to(device)
+        us = graph_us(lambda: cache.write_slots(slots, k, v, 0, validate=False))
+        nbytes = 2 * tokens * hkv * d * (2 + 2) + 8 * tokens
+        out[str(tokens)] = {"us": round(us, 3), "net_us": round(us - node_us, 3),
+                            "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1)}
+    del cache
+    return {"workload": "kv_write_qwen05b_bf16", "calls_per_graph": calls_per_graph,
+            "graph_node_us": round(node_us, 3), "by_tokens": out,
+            "note": "latency-bound: at 64 tokens a call costs about one graph node; "
+                    "every call rewrites the same rows from the same sources, which stay "
+                    "in the 256 MB MALL, so GBps is a cache figure, not an HBM one; in "
+                    "the decode step the write runs inside the decode launch "
+                    "(mlr_paged_decode_append)"}
+
+
 SPLITS_32K = (0, 4, 8, 16, 32, 64)
 POOLS_32K = 3
 
@@ -1150,6 +1200,7 @@ def main():
         line["pre_attention"] = bench_pre_attention(device)
         line["pre_attention"]["roofline"]["traffic"] = (
             traffic.get("pre_attention_call_bytes") if traffic else None)
+    line["kv_write"] = bench_kv_write(device)
     line["decode_32k"] = bench_decode_32k(device)
     line["decode_32k"]["traffic"] = traffic.get("decode_32k_bytes") if traffic else None
     line["accumulator"] = bench_accumulator(device)
