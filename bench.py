@@ -32,7 +32,8 @@ launch) and the same step as two launches (fused pre-attention kernel, then
 decode); the
 read floor of the decode step (config.read_floor: a read-only pass over the
 same K/V rows through the same block tables, mlr_paged_kv_read_floor); the
-8 x 32K decode over rotated pools; the fused pre-attention step; and
+8 x 32K decode over rotated pools; the fused pre-attention step; the KV
+write on its own (``kv_write``); the FP32 batch-4 decode step; and
 ``serving``, end-to-end continuous-batching steps of a random-init
 Qwen2.5-0.5B-shape model in BF16 (workloads.qwen05b_serving: about 48
 decodes + 2 x 1024-token prefills per step, 128 steps after the warm-up).
@@ -44,9 +45,11 @@ decodes + 2 x 1024-token prefills per step, 128 steps after the warm-up).
 ``--steps`` decode steps over the rotated layers, one decode without the
 fused write and one one-launch served step per layer, the read floor per
 layer, ten prefill calls, the
-fused pre-attention kernel, and a plain 1 GiB device copy whose FETCH_SIZE /
-WRITE_SIZE counters calibrate the traffic counters (the copy reads and
-writes exactly 1 GiB).
+fused pre-attention kernel, the 8 x 32K decode, the FP32 batch-4 step, and a
+plain 1 GiB device copy whose FETCH_SIZE / WRITE_SIZE counters calibrate the
+traffic counters (the copy reads and writes exactly 1 GiB). With
+``--contiguous-only`` it launches only the contiguous-placement comparators
+of the decode step.
 """
 
 from __future__ import annotations
