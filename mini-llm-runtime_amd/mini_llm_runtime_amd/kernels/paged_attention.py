@@ -100,7 +100,9 @@ def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def check_workspace(workspace: torch.Tensor) -> None:
     """Raise DecodeMergeError when `workspace`'s merge-failure flag is set
     (after clearing the workspace); synchronises torch's current stream and
-    must run outside graph capture (mlr_paged_decode_workspace_check)."""
+    must run outside graph capture (mlr_paged_decode_workspace_check). Work
+    that other streams queued on the workspace must have finished first
+    (check_decode_workspaces synchronises the device for that)."""
     lib = _lib.load()
     device = workspace.device
     with torch.cuda.device(device):
