@@ -89,6 +89,11 @@ def test_workspace_size_is_host_arithmetic():
                                           16, 2, 64, 1 << 22, 4, 4, 1 << 23, 1 << 24, 2, 14,
                                           0.125, 0, 0, 1 << 25, 1 << 30, 1 << 26, 896, 64,
                                           None), b"needs bf16"),
+    # The workspace check validates its arguments before touching the stream.
+    (lambda lib: lib.mlr_paged_decode_workspace_check(None, 4096, None), b"flag region"),
+    (lambda lib: lib.mlr_paged_decode_workspace_check(1 << 20, 128, None), b"flag region"),
+    (lambda lib: lib.mlr_paged_decode_workspace_check((1 << 20) + 64, 4096, None),
+     b"256-byte aligned"),
 ])
 def test_argument_errors_return_before_any_launch(call, needle):
     lib = _lib.load()
