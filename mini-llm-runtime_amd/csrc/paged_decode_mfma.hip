@@ -158,9 +158,10 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Reductions over the 16 lanes of row 0 (lanes 0..15) with DPP moves inside
-// the row (quad xor 1, quad xor 2, half-row mirror, row mirror): afterwards
-// every lane of the row holds the result. VALU only, no LDS permutes.
+// Reductions over each 16-lane row of a wave (lanes 16r .. 16r + 15) with DPP
+// moves inside the row (quad xor 1, quad xor 2, half-row mirror, row mirror):
+// afterwards every lane of the row holds its row's result. VALU only, no LDS
+// permutes; every lane of the row must be active.
 template <int kCtrl>
 __device__ __forceinline__ float dpp_move(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
@@ -176,9 +177,6 @@ __device__ __forceinline__ float row_sum16(float x) {
   x += dpp_move<0x4E>(x);
   x += dpp_move<0x141>(x);
   return x + dpp_move<0x140>(x);
-}
-__device__ __forceinline__ float lane_value(float x, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
 template <int D>
@@ -967,7 +965,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // The group merge, in split order: splits 0 .. nsplits - 2 from the
   // workspace, kChunk per round trip, and this workgroup's own split folded
   // in with the last chunk:
-  //   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s.
+  //   M = max_s m_s,  out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s
+  // (the numerators add in split order; a chunk's part of the denominator is
+  // a reduction over its 16 splits).
   // A chunk is read again until every word of it has arrived (none is zero).
   // Its producers are workgroups of lower index, dispatched before this one:
   // they hold or held a slot and finish without waiting on anything, so the
@@ -978,8 +978,6 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   constexpr int kChunk = 16;
   constexpr int kMaxPolls = 1 << 17;
   static_assert(kSplitRowPad % kChunk == 0, "a chunk's rows stay inside one head's rows");
-  __shared__ float mc_s[16][kChunk];   // the chunk's m per (head, split)
-  __shared__ float lc_s[16][kChunk];   // the chunk's l per (head, split)
   __shared__ float f_s[kChunk + 1][16];  // 2^{m_s - M_new}: the chunk's splits, then own
   __shared__ float rescale_s[16];      // 2^{M_old - M_new} per head
   __shared__ float den_s[16];
@@ -1092,31 +1090,28 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
           __builtin_amdgcn_raw_buffer_store_b32(0u, ml_r, mloff, 0, kCoherent);
           __builtin_amdgcn_raw_buffer_store_b32(0u, ml_r, mloff + 4u, 0, kCoherent);
         }
+        // The chunk's weights, one (head mh, split s0 + ms) per thread: the
+        // 16 threads of a head are one 16-lane row of a wave, so the head's
+        // new reference point and its part of the denominator are DPP
+        // reductions inside the row. Rows past cnt weigh 0 (their l word is
+        // zero, read as -0).
         if (mh < 16) {
-          mc_s[mh][ms] = ms < cnt ? unpublish(mw) : -INFINITY;
-          lc_s[mh][ms] = unpublish(lw);
-        }
-        __syncthreads();
-        if (threadIdx.x < ngh) {
-          const int h = threadIdx.x;
-          float m_new = mrun_s[h];
-#pragma unroll
-          for (int s = 0; s < kChunk; ++s) m_new = fmaxf(m_new, mc_s[h][s]);
+          const int h = mh;
+          const float m_old = mrun_s[h];
+          const float mc = ms < cnt ? unpublish(mw) : -INFINITY;
+          float m_new = row_max16(fmaxf(m_old, mc));
           if (last) m_new = fmaxf(m_new, own_m_s[h]);
-          const float rs = __builtin_amdgcn_exp2f(mrun_s[h] - m_new);  // 0 on the first chunk
-          float den = den_s[h] * rs;
-#pragma unroll
-          for (int s = 0; s < kChunk; ++s) {
-            const float f = s < cnt ? __builtin_amdgcn_exp2f(mc_s[h][s] - m_new) : 0.f;
-            f_s[s][h] = f;
-            den += f * lc_s[h][s];
+          const float f = ms < cnt ? __builtin_amdgcn_exp2f(mc - m_new) : 0.f;
+          const float part = row_sum16(f * unpublish(lw));
+          f_s[ms][h] = f;
+          if (ms == 0) {
+            const float rs = __builtin_amdgcn_exp2f(m_old - m_new);  // 0 on the first chunk
+            const float f_own = last ? __builtin_amdgcn_exp2f(own_m_s[h] - m_new) : 0.f;
+            f_s[kChunk][h] = f_own;
+            rescale_s[h] = rs;
+            den_s[h] = den_s[h] * rs + part + f_own * own_l_s[h];
+            mrun_s[h] = m_new;
           }
-          const float f_own = last ? __builtin_amdgcn_exp2f(own_m_s[h] - m_new) : 0.f;
-          f_s[kChunk][h] = f_own;
-          den += f_own * own_l_s[h];
-          rescale_s[h] = rs;
-          den_s[h] = den;
-          mrun_s[h] = m_new;
         }
         __syncthreads();
       }
