@@ -365,9 +365,10 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                        (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0 &&
                        (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 &&
                        q_stride_b % 8 == 0 && q_stride_h % 8 == 0;
-  // The matrix-core kernel keeps token positions in 32 bits.
+  // The matrix-core kernel keeps token positions in 32 bits, and the byte
+  // offsets of a GQA group's q rows (group x q_stride_h elements).
   const bool mfma =
-      aligned && max_context < (int64_t(1) << 31) &&
+      aligned && max_context < (int64_t(1) << 31) && q_stride_h < (int64_t(1) << 20) &&
       decode_mfma_eligible(dtype, head_dim, num_q_heads / num_kv_heads, block_size);
   int64_t ts = tokens_per_split > 0 ? tokens_per_split
                                     : default_tokens_per_split(mfma, head_dim, max_context, dtype);

@@ -610,14 +610,22 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // depend on one another, so both loads are issued before either is used.
   // Block ids are read for every tile position the split could hold, within
   // the table's width.
+  // The GQA group's q rows lie under one buffer resource; lanes past the
+  // group read beyond its range and get zeros. No branch and no select, so
+  // nothing makes the compiler wait for these loads before it issues the
+  // block-id and tile loads (a conditional load here did, on the rotary
+  // variant: one more memory round trip ahead of the tile loads).
   const bool head_ok = m16 < p.group;
-  const S *qrow = static_cast<const S *>(p.q) + b * p.q_sb +
-                  (int64_t)(kvh * p.group + (head_ok ? m16 : 0)) * p.q_sh;
+  const uint32_t q_bytes =
+      static_cast<uint32_t>(((int64_t)(p.group - 1) * p.q_sh + D) * kSize);
+  const __amdgpu_buffer_rsrc_t q_r = block_rsrc(
+      static_cast<const S *>(p.q) + b * p.q_sb + (int64_t)(kvh * p.group) * p.q_sh, q_bytes);
+  const uint32_t q_off = head_ok ? static_cast<uint32_t>(m16 * p.q_sh * kSize) : q_bytes;
   uint4 qraw[QK];
 #pragma unroll
   for (int j = 0; j < QK; ++j)
-    qraw[j] = head_ok ? *reinterpret_cast<const uint4 *>(qrow + 4 * kE * j + kE * g)
-                      : make_uint4(0, 0, 0, 0);
+    qraw[j] = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(q_r, q_off + (4 * kE * j + kE * g) * kSize, 0, 0));
   // Token positions fit in 32 bits here (max_blocks * block_size < 2^31;
   // speculative tile positions stay below 2^32): block index and offset by
   // shift and mask when block_size is a power of two, else 32-bit division.
@@ -666,7 +674,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   constexpr bool rope = kRope;
   __shared__ float rope_s[kWaves * kH][D];  // cos at [i], sin at [d/2 + i]
   float rope_freq = 0.f;
-  if (rope && lane < D / 2) rope_freq = p.inv_freq[lane];
+  // Every lane loads (lanes past d/2 a duplicate, never used): no branch.
+  if (rope) rope_freq = p.inv_freq[lane & (D / 2 - 1)];
 
   const int ntiles = static_cast<int>(ceil_div(t1 - t0, 16));
 

@@ -240,21 +240,14 @@ void prefill_mfma(PrefillParams p) {
   const int qpos = prefix + qi;
   const uint16_t *qrow = static_cast<const uint16_t *>(p.q) +
                          (rg.q0 + (q_ok ? qi : 0)) * p.q_st + static_cast<int64_t>(h) * p.q_sh;
-  // Pre-multiplied by scale*log2(e): the scores come out in base-2 units.
-  const float c2 = static_cast<float>(p.scale) * kLog2e;
+  // Issued here and turned into fragments after the prologue's copies have
+  // been issued and waited for: the row address is clamped, so the loads
+  // are unconditional (a load under a branch made the compiler wait for it
+  // before issuing the block-id loads and the first copies).
+  uint4 qraw[QS];
+#pragma unroll
+  for (int s = 0; s < QS; ++s) qraw[s] = *reinterpret_cast<const uint4 *>(qrow + 16 * s + 8 * hh);
   bf16x8_t qf[QS];
-#pragma unroll
-  for (int s = 0; s < QS; ++s) {
-    const uint4 raw = q_ok ? *reinterpret_cast<const uint4 *>(qrow + 16 * s + 8 * hh)
-                           : make_uint4(0, 0, 0, 0);
-    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-    uint32_t o4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      o4[e] = bf16_pack2(__uint_as_float(w4[e] << 16) * c2,
-                         __uint_as_float(w4[e] & 0xffff0000u) * c2);
-    qf[s] = __builtin_bit_cast(bf16x8_t, make_uint4(o4[0], o4[1], o4[2], o4[3]));
-  }
 
   // Copy role: copy i of a span moves chunk positions [64i, 64i + 64) of its 16
   // rows; lane l fills position 64i + l (row rr, physical chunk pc) with
@@ -554,8 +547,22 @@ void prefill_mfma(PrefillParams p) {
     dk = span_of(t_lo + 1, id1);
     issue_span(dk, p.kc, ks1[split], badk1[split]);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's prologue copies and flags
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's prologue copies and flags, and q
   __builtin_amdgcn_s_barrier();
+  // Q pre-multiplied by scale*log2(e) (the scores come out in base-2 units);
+  // rows past the chunk are zero.
+  const float c2 = static_cast<float>(p.scale) * kLog2e;
+#pragma unroll
+  for (int s = 0; s < QS; ++s) {
+    const uint4 raw = q_ok ? qraw[s] : make_uint4(0, 0, 0, 0);
+    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+    uint32_t o4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o4[e] = bf16_pack2(__uint_as_float(w4[e] << 16) * c2,
+                         __uint_as_float(w4[e] & 0xffff0000u) * c2);
+    qf[s] = __builtin_bit_cast(bf16x8_t, make_uint4(o4[0], o4[1], o4[2], o4[3]));
+  }
   if (split == 1) __builtin_amdgcn_s_barrier();
   // S^T (M to V) and packed P (V to M) are defined in every phase, idle
   // ones included, so neither is live across the phase that does not use it.
@@ -663,9 +670,14 @@ void prefill_mfma(PrefillParams p) {
   }
 
   const float l_tot = pair_sum(l_run);
-  if (q_ok) {
+  // The lane's query and half are recomputed from the lane id here rather
+  // than kept in registers across the main loop (which spilled them).
+  int lane_e = __lane_id();
+  asm volatile("" : "+v"(lane_e));
+  const int qi_e = wq + (lane_e & 31), hh_e = lane_e >> 5;
+  if (qi_e < qlen) {
     const float inv = 1.f / l_tot;
-    uint16_t *orow = static_cast<uint16_t *>(p.out) + (rg.q0 + qi) * p.o_st +
+    uint16_t *orow = static_cast<uint16_t *>(p.out) + (rg.q0 + qi_e) * p.o_st +
                      static_cast<int64_t>(h) * p.o_sh;
 #pragma unroll
     for (int n = 0; n < NB; ++n)
@@ -678,7 +690,7 @@ void prefill_mfma(PrefillParams p) {
                 ((uint32_t)float_to_bf16_bits(a[4 * g4 + 1] * inv) << 16),
             (uint32_t)float_to_bf16_bits(a[4 * g4 + 2] * inv) |
                 ((uint32_t)float_to_bf16_bits(a[4 * g4 + 3] * inv) << 16));
-        *reinterpret_cast<uint2 *>(orow + 32 * n + 8 * g4 + 4 * hh) = v;
+        *reinterpret_cast<uint2 *>(orow + 32 * n + 8 * g4 + 4 * hh_e) = v;
       }
   }
 }
