@@ -177,6 +177,111 @@ __global__ __launch_bounds__(256) void qkv_rope_write_kernel(
   }
 }
 
+// Head size 64 or 128 with 16-byte chunks (the same arithmetic as above,
+// the chunk-to-head map by shifts). The token index is made wave-uniform, so
+// its position and slot are scalar loads, and a pass's row loads are issued
+// before anything waits: the cos/sin table is built while they are in flight.
+template <typename T, typename I, int D, int K>
+__global__ __launch_bounds__(256) void qkv_rope_write_wide_kernel(
+    const T *__restrict__ qkv, int64_t qkv_st, const T *__restrict__ bias,
+    const int64_t *__restrict__ positions, const float *__restrict__ inv_freq,
+    const void *__restrict__ slots, T *__restrict__ q_out, int64_t q_st,
+    T *__restrict__ kc, T *__restrict__ vc, int64_t num_slots, int64_t num_tokens, int hq,
+    int hkv) {
+#pragma clang fp contract(off)
+  constexpr int kVec = 16 / sizeof(T);
+  constexpr int kHalf = D / 2;
+  constexpr int kCph = kHalf / kVec;  // rotary chunks per head
+  static_assert(kHalf % kVec == 0 && kHalf <= 64, "head size 64 or 128");
+  using V = Vec<T, kVec>;
+  extern __shared__ float cs_all[];  // per wave: [D/2] cos then [D/2] sin
+  const int lane = __lane_id();
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
+  float *cs = cs_all + wv * D;
+  const int n_rope = (hq + hkv) * kCph;
+  const int n_chunks = n_rope + hkv * (D / kVec);
+  const int v_base = (hq + hkv) * D;
+  // Lanes past D/2 load a duplicate they never use.
+  const float my_freq = inv_freq[lane & (kHalf - 1)];
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * waves + wv; t < num_tokens;
+       t += static_cast<int64_t>(gridDim.x) * waves) {
+    const T *row = qkv + t * qkv_st;
+    V lo[K], hi[K];
+    // Chunk c of the row: rotary chunks first (head c / kCph, elements
+    // [i0, i0 + kVec) and their partners at + D/2), then the v chunks.
+    auto load_pass = [&](int c0) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int c = min(c0 + 64 * k + lane, n_chunks - 1);
+        const bool rope = c < n_rope;
+        const int e = rope ? (c / kCph) * D + (c % kCph) * kVec : v_base + (c - n_rope) * kVec;
+        lo[k] = *reinterpret_cast<const V *>(row + e);
+        hi[k] = *reinterpret_cast<const V *>(row + (rope ? e + kHalf : e));
+      }
+    };
+    load_pass(0);
+    const float pos = static_cast<float>(positions[t]);
+    const int64_t slot = load_index<I>(slots, t);
+    const bool write_kv = slot >= 0 && slot < num_slots;
+    if (lane < kHalf) {
+      // sincosf: one argument reduction for both; its results are those of
+      // cosf and sinf.
+      float sv, cv;
+      sincosf(pos * my_freq, &sv, &cv);
+      rnd2<T>(cv, sv);
+      cs[lane] = cv;
+      cs[kHalf + lane] = sv;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int c0 = 0;;) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int c = c0 + 64 * k + lane;
+        if (c >= n_chunks) continue;
+        if (c < n_rope) {
+          const int h = c / kCph, i0 = (c % kCph) * kVec;
+          V olo, ohi;
+#pragma unroll
+          for (int j = 0; j < kVec; ++j) {
+            float x_lo = Elem<T>::to_f32(lo[k].v[j]), x_hi = Elem<T>::to_f32(hi[k].v[j]);
+            if (bias != nullptr) {
+              x_lo = rnd<T>(x_lo + load_f(bias + h * D + i0 + j));
+              x_hi = rnd<T>(x_hi + load_f(bias + h * D + kHalf + i0 + j));
+            }
+            const float cv = cs[i0 + j], sv = cs[kHalf + i0 + j];
+            float a = x_lo * cv, b = -x_hi * sv, e = x_hi * cv, f = x_lo * sv;
+            rnd2<T>(a, b);
+            rnd2<T>(e, f);
+            olo.v[j] = Elem<T>::from_f32(a + b);
+            ohi.v[j] = Elem<T>::from_f32(e + f);
+          }
+          T *o = h < hq ? q_out + t * q_st + static_cast<int64_t>(h) * D
+                        : kc + (slot * hkv + (h - hq)) * D;
+          if (h < hq || write_kv) {
+            *reinterpret_cast<V *>(o + i0) = olo;
+            *reinterpret_cast<V *>(o + i0 + kHalf) = ohi;
+          }
+        } else if (write_kv) {
+          const int ev = (c - n_rope) * kVec;  // element within the token's v heads
+          V ov = lo[k];
+          if (bias != nullptr) {
+#pragma unroll
+            for (int j = 0; j < kVec; ++j)
+              ov.v[j] = Elem<T>::from_f32(Elem<T>::to_f32(lo[k].v[j]) +
+                                          load_f(bias + v_base + ev + j));
+          }
+          *reinterpret_cast<V *>(vc + slot * hkv * D + ev) = ov;
+        }
+      }
+      c0 += 64 * K;
+      if (c0 >= n_chunks) break;
+      load_pass(c0);
+    }
+    __builtin_amdgcn_wave_barrier();  // cs is rewritten for the next token
+  }
+}
+
 template <typename T, typename I, int VEC>
 void launch_vec(const void *qkv, int64_t qkv_st, const void *bias, const int64_t *positions,
                 const float *inv_freq, const void *slots, void *q_out, int64_t q_st, void *kc,
@@ -196,30 +301,60 @@ void launch_vec(const void *qkv, int64_t qkv_st, const void *bias, const int64_t
       num_slots, num_tokens, hq, hkv, d);
 }
 
+template <typename T, typename I, int D>
+void launch_wide(const void *qkv, int64_t qkv_st, const void *bias, const int64_t *positions,
+                 const float *inv_freq, const void *slots, void *q_out, int64_t q_st, void *kc,
+                 void *vc, int64_t num_slots, int64_t num_tokens, int hq, int hkv,
+                 hipStream_t stream) {
+  const int waves = num_tokens >= 1024 ? 4 : 1;
+  const int64_t wgs = (num_tokens + waves - 1) / waves;
+  const int64_t blocks = wgs < 65536 ? wgs : 65536;
+  const size_t lds = static_cast<size_t>(waves) * D * sizeof(float);
+  qkv_rope_write_wide_kernel<T, I, D, 2>
+      <<<static_cast<unsigned>(blocks), 64 * waves, lds, stream>>>(
+          static_cast<const T *>(qkv), qkv_st, static_cast<const T *>(bias), positions,
+          inv_freq, slots, static_cast<T *>(q_out), q_st, static_cast<T *>(kc),
+          static_cast<T *>(vc), num_slots, num_tokens, hq, hkv);
+}
+
 template <typename T>
 int launch(const void *qkv, int64_t qkv_st, const void *bias, const int64_t *positions,
            const float *inv_freq, const void *slots, int index_dtype, void *q_out,
            int64_t q_st, void *kc, void *vc, int64_t num_slots, int64_t num_tokens, int hq,
            int hkv, int d, hipStream_t stream) {
-  // Four-element chunks need half a head to be whole chunks and every row
-  // start aligned to the chunk size.
+  // 16-byte chunks at head sizes 64 and 128; otherwise four-element chunks.
+  // Either needs half a head to be whole chunks and every row start aligned
+  // to the chunk size.
+  auto aligned_to = [&](int vec) {
+    const uintptr_t align = vec * sizeof(T) - 1;
+    return (d / 2) % vec == 0 && qkv_st % vec == 0 && q_st % vec == 0 &&
+           (reinterpret_cast<uintptr_t>(qkv) & align) == 0 &&
+           (reinterpret_cast<uintptr_t>(q_out) & align) == 0 &&
+           (reinterpret_cast<uintptr_t>(kc) & align) == 0 &&
+           (reinterpret_cast<uintptr_t>(vc) & align) == 0;
+  };
+  constexpr int kWide = 16 / sizeof(T);
   constexpr int kVec = 4;
-  const uintptr_t align = kVec * sizeof(T) - 1;
-  const bool vec = (d / 2) % kVec == 0 && qkv_st % kVec == 0 && q_st % kVec == 0 &&
-                   (reinterpret_cast<uintptr_t>(qkv) & align) == 0 &&
-                   (reinterpret_cast<uintptr_t>(q_out) & align) == 0 &&
-                   (reinterpret_cast<uintptr_t>(kc) & align) == 0 &&
-                   (reinterpret_cast<uintptr_t>(vc) & align) == 0;
+  const bool wide = (d == 64 || d == 128) && aligned_to(kWide);
+  const bool vec = aligned_to(kVec);
   const bool i32 = index_dtype == MLR_INDEX_I32;
+#define MLR_QKV_WIDE(I, D)                                                                  \
+  launch_wide<T, I, D>(qkv, qkv_st, bias, positions, inv_freq, slots, q_out, q_st, kc, vc, \
+                       num_slots, num_tokens, hq, hkv, stream)
 #define MLR_QKV_LAUNCH(I, V)                                                                  \
   launch_vec<T, I, V>(qkv, qkv_st, bias, positions, inv_freq, slots, q_out, q_st, kc, vc,   \
                       num_slots, num_tokens, hq, hkv, d, stream)
-  if (vec) {
+  if (wide && d == 64) {
+    if (i32) MLR_QKV_WIDE(int32_t, 64); else MLR_QKV_WIDE(int64_t, 64);
+  } else if (wide) {
+    if (i32) MLR_QKV_WIDE(int32_t, 128); else MLR_QKV_WIDE(int64_t, 128);
+  } else if (vec) {
     if (i32) MLR_QKV_LAUNCH(int32_t, kVec); else MLR_QKV_LAUNCH(int64_t, kVec);
   } else {
     if (i32) MLR_QKV_LAUNCH(int32_t, 1); else MLR_QKV_LAUNCH(int64_t, 1);
   }
 #undef MLR_QKV_LAUNCH
+#undef MLR_QKV_WIDE
   return check_launch("mlr_qkv_rope_write");
 }
 
