@@ -754,8 +754,36 @@ def bench_decode_32k(device, reps=4, calls_per_graph=6):
         sweep["default" if splits == 0 else str(splits)] = round(us, 2)
     best = min(sweep, key=sweep.get)
     best_us = sweep[best]
+
+    # Read floor of the same step: a read-only pass over the same K/V rows
+    # through the same block tables and rotated pools, 512-token items (the
+    # floor kernel's best item size at this length).
+    floor_items = 512
+    floor_out = torch.empty(8 * -(-bt.shape[1] * 16 // floor_items), dtype=torch.int32,
+                            device=device)
+
+    def floor_step(i):
+        kc, vc = pools[i % POOLS_32K]
+        kpa.paged_kv_read_floor(kc, vc, bt, ctx, tokens_per_item=floor_items, out=floor_out)
+
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        for i in range(POOLS_32K):
+            floor_step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(calls_per_graph):
+            floor_step(i)
+    warm_graph(g, stream)
+    floor_us = timed_graph(g, reps, stream) / (reps * calls_per_graph) * 1e6
+    kv_bytes = wl.algorithmic_bytes()
     return {"workload": wl.name, "step_bytes": nbytes, "pools_rotated": POOLS_32K,
             "us_by_splits": sweep, "best": best,
+            "read_floor": {"tokens_per_item": floor_items, "us": round(floor_us, 2),
+                           "GBps": round(kv_bytes / floor_us / 1e3, 1),
+                           "frac_of_hbm_peak": round(kv_bytes / floor_us / 1e3 / HBM_PEAK_GBS, 4),
+                           "step_over_floor": round(sweep["default"] / floor_us, 3)},
             "GBps_default": round(nbytes / sweep["default"] / 1e3, 1),
             "frac_of_hbm_peak_default": round(nbytes / sweep["default"] / 1e3 / HBM_PEAK_GBS, 4),
             "GBps_best": round(nbytes / best_us / 1e3, 1),

@@ -1,13 +1,14 @@
 // bf16 and FP32 split-KV paged decode on gfx950 matrix cores, in one launch.
 //
 // One workgroup of four wavefronts per (live split, KV head), or of eight per
-// (live split, pair of KV heads), four for each head. A split is
+// (live split, pair of KV heads), four for each head (FP32 grids that leave
+// most CUs idle: eight wavefronts per KV head). A split is
 // tokens_per_split tokens of one sequence; the live splits of all sequences
 // are numbered sequence by sequence and every workgroup finds its own from a
 // prefix sum of the context lengths, so no workgroup is spent on a split past
 // a sequence's end (only the grid's tail, sized for the widest table, exits
 // at once). The split's
-// 16-token tiles are dealt round-robin to a head's four waves; each wave keeps the
+// 16-token tiles are dealt round-robin to a head's waves; each wave keeps the
 // online-softmax state of all (<= 16) query heads of the KV head's GQA group,
 // so every K/V byte is read from HBM exactly once for the whole group.
 //
@@ -30,7 +31,7 @@
 // kBatch tiles at once and the next batch's loads before computing the
 // current one (two register buffers), so 8-16 KiB per wave are in flight.
 //
-// A KV head's four waves merge through LDS. A sequence that fits one split writes its
+// A KV head's waves merge through LDS. A sequence that fits one split writes its
 // output directly; otherwise every split but the last stores its (m, l, acc)
 // to the workspace with device-coherent stores, each word encoded so that
 // zero means "not stored yet", and the workgroup of the last split (the
@@ -63,7 +64,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // waves per KV head, unless a launch picks another count
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int D> struct VRow;
@@ -575,12 +576,12 @@ __device__ __forceinline__ void publish(__amdgpu_buffer_rsrc_t r, uint32_t off, 
 __device__ __forceinline__ float unpublish(uint32_t w) { return __uint_as_float(w ^ 0x80000000u); }
 
 // One work item (a split of one sequence, one KV head) for the workgroup.
-// kH KV heads per workgroup (1 or 2), kWaves waves each: waves
-// hs * kWaves .. + kWaves - 1 serve KV head kvh_base + hs over the same
+// kH KV heads per workgroup (1 or 2), kW waves each: waves
+// hs * kW .. + kW - 1 serve KV head kvh_base + hs over the same
 // tiles, so with kH = 2 both halves of every slot row are requested by one
 // workgroup at the same time.
 template <typename T, int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH,
-          bool kRope>
+          bool kRope, int kW>
 __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkItem &it,
                                             int kvh_base) {
   constexpr bool kF32 = std::is_same<T, float>::value;
@@ -592,13 +593,13 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   constexpr int kE = 16 / kSize;          // elements per 16-byte chunk
   constexpr int kRowChunks = D / kE;      // 16-byte chunks per K (or V) row of one head
   constexpr int VC = D / 16;
-  constexpr int kThreads = 64 * kWaves * kH;
+  constexpr int kThreads = 64 * kW * kH;
   const int lane = threadIdx.x & 63;
   // The wave index is uniform within a wave; saying so keeps every value
   // derived from it (tile counts, block ids, descriptors) in SGPRs.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int w = wave % kWaves;   // the wave's place among its KV head's waves
-  const int hs = wave / kWaves;  // which of the workgroup's KV heads it serves
+  const int w = wave % kW;   // the wave's place among its KV head's waves
+  const int hs = wave / kW;  // which of the workgroup's KV heads it serves
   const int kvh = kvh_base + hs;
   const int m16 = lane & 15, g = lane >> 4;
   const int b = it.b, split = it.split, nsplits = it.ns;
@@ -639,7 +640,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     return bs_pow2 ? (pos & (bs32 - 1)) : pos % bs32;
   };
   auto raw_block_id = [&](int k) -> int64_t {
-    const int64_t idx = block_of(static_cast<uint32_t>(t0) + 16u * (w + kWaves * k));
+    const int64_t idx = block_of(static_cast<uint32_t>(t0) + 16u * (w + kW * k));
     return idx < p.max_blocks ? bt_row[idx] : int64_t(-1);
   };
   int64_t blk_raw = raw_block_id(lane);
@@ -653,7 +654,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   const bool append_here = kAppend && last_pos >= t0 && last_pos < t1;
   const int last_rel = static_cast<int>(last_pos - t0) & ~15;  // tile of ctx - 1
   const int last_tok = static_cast<int>(last_pos - t0) & 15;   // its row
-  const bool new_owner = append_here && w == (last_rel >> 4) % kWaves;  // uniform
+  const bool new_owner = append_here && w == (last_rel >> 4) % kW;  // uniform
   __shared__ __align__(16) S new_row_s[kH][2 * D];
   const int64_t new_slot = kAppend ? p.new_slots[b] : -1;
   const bool new_is_v = lane >= kRowChunks;
@@ -672,7 +673,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // could only be used once they had all landed.
   static_assert(kAppend || !kRope, "the rotary embedding rides on the fused write");
   constexpr bool rope = kRope;
-  __shared__ float rope_s[kWaves * kH][D];  // cos at [i], sin at [d/2 + i]
+  __shared__ float rope_s[kW * kH][D];  // cos at [i], sin at [d/2 + i]
   float rope_freq = 0.f;
   // Every lane loads (lanes past d/2 a duplicate, never used): no branch.
   if (rope) rope_freq = p.inv_freq[lane & (D / 2 - 1)];
@@ -733,7 +734,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 
   // This wave's tiles: w, w + 4, w + 8, ...; block id of the wave's k-th
   // tile lives in lane (k % 64) of blk_reg (-1: no tile or invalid id).
-  const int nk = ntiles > w ? (ntiles - w + kWaves - 1) / kWaves : 0;
+  const int nk = ntiles > w ? (ntiles - w + kW - 1) / kW : 0;
   auto valid_id = [&](int k, int64_t raw) -> int {
     return (k < nk && raw >= 0 && raw < p.num_blocks) ? static_cast<int>(raw) : -1;
   };
@@ -812,7 +813,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     for (int u = 0; u < kBatch; ++u) {
       const int k = kb + u;
       const int blk = k < nk ? __builtin_amdgcn_readlane(blk_reg, k & 63) : -1;
-      const int rel = 16 * (w + kWaves * k);
+      const int rel = 16 * (w + kW * k);
       // Byte offset of the tile's first token inside its block.
       const int tile_off =
           static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel)) * row_elems * kSize;
@@ -822,7 +823,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int k = kb + u;
-        if (k < nk && 16 * (w + kWaves * k) == last_rel) mark_new_row(buf[u]);
+        if (k < nk && 16 * (w + kW * k) == last_rel) mark_new_row(buf[u]);
       }
     }
   };
@@ -855,10 +856,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     // workgroup keeps 80 KB in flight and the splits of a batch like 64
     // sequences of up to 4K tokens fit the GPU in one generation.
     static_assert(D == 64 && kBatch == 4 && !kF32, "LDS landing is laid out for bf16 head_dim 64");
-    __shared__ __align__(16) unsigned char lds_tiles[kWaves * kH][kLdsTileBytes];
+    __shared__ __align__(16) unsigned char lds_tiles[kW * kH][kLdsTileBytes];
     Tile<T, D> buf[kBatch];
     issue(buf, 0);
-    const int rel4 = 16 * (w + kWaves * kBatch);
+    const int rel4 = 16 * (w + kW * kBatch);
     const int blk4 = kBatch < nk ? __builtin_amdgcn_readlane(blk_reg, kBatch) : -1;
     copy_tile_to_lds(lds_tiles[wave], kc, vc, block_elems,
                      static_cast<int>(in_block(static_cast<uint32_t>(t0) + rel4)) * row_elems * 2,
@@ -887,9 +888,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // Per-head l: sum the four lanes that share the head.
   st.l = sum_xor32(sum_xor16(st.l));
 
-  __shared__ float o_s[kWaves * kH][16][D + 4];
-  __shared__ float m_s[kWaves * kH][16];
-  __shared__ float l_s[kWaves * kH][16];
+  __shared__ float o_s[kW * kH][16][D + 4];
+  __shared__ float m_s[kW * kH][16];
+  __shared__ float l_s[kW * kH][16];
   if (g == 0) {
     m_s[wave][m16] = st.m;
     l_s[wave][m16] = st.l;
@@ -928,7 +929,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       reinterpret_cast<float *>(p.ws_ml) + row_b * p.split_stride * 2, 0,
       static_cast<uint32_t>(rows_g) * 8u, 0x00020000);
   const bool merger = nsplits > 1 && split == nsplits - 1;
-  constexpr int kMaxOut = (16 * D + kThreads - 1) / kThreads;  // outputs per thread, at most
+  // Outputs per thread, at most (at least the merge's kPre per pass).
+  constexpr int kMaxOut = (16 * D + kThreads - 1) / kThreads < 2 ? 2
+                                                                  : (16 * D + kThreads - 1) / kThreads;
   const int nout = ngh * D;
   float own[kMaxOut];
   __shared__ float own_m_s[16], own_l_s[16];
@@ -938,15 +941,15 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     own[r] = 0.f;
     if (idx < nout) {
       const int h = idx / D, d = idx % D;
-      // Waves w0 .. w0 + kWaves - 1 hold head h (head hg of their group).
-      const int w0 = kH == 1 ? 0 : (h / p.group) * kWaves;
+      // Waves w0 .. w0 + kW - 1 hold head h (head hg of their group).
+      const int w0 = kH == 1 ? 0 : (h / p.group) * kW;
       const int hg = kH == 1 ? h : h % p.group;
       float M = m_s[w0][hg];
 #pragma unroll
-      for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, m_s[w0 + ww][hg]);
+      for (int ww = 1; ww < kW; ++ww) M = fmaxf(M, m_s[w0 + ww][hg]);
       float num = 0.f, den = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) {
+      for (int ww = 0; ww < kW; ++ww) {
         const float f = __builtin_amdgcn_exp2f(m_s[w0 + ww][hg] - M);
         num += f * o_s[w0 + ww][hg][d];
         den += f * l_s[w0 + ww][hg];
@@ -1177,13 +1180,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 // table and the workgroups past the live items exit after the context
 // lengths.
 template <typename T, int D, int kBatch, bool kDouble, bool kAppend, bool kLds, int kH,
-          bool kRope>
-__global__ __launch_bounds__(64 * kWaves * kH) void decode_mfma(DecodeParams p) {
+          bool kRope, int kW>
+__global__ __launch_bounds__(64 * kW * kH) void decode_mfma(DecodeParams p) {
   const int64_t cap = p.max_blocks * p.block_size;
   const int nhg = p.hkv / kH;  // KV-head groups per item
   const WorkItem it = find_item(p, blockIdx.x / nhg, cap);
   if (it.b < 0) return;  // uniform
-  decode_item<T, D, kBatch, kDouble, kAppend, kLds, kH, kRope>(p, it, (blockIdx.x % nhg) * kH);
+  decode_item<T, D, kBatch, kDouble, kAppend, kLds, kH, kRope, kW>(p, it,
+                                                                  (blockIdx.x % nhg) * kH);
 }
 
 }  // namespace
@@ -1195,28 +1199,28 @@ bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
          block_size % 16 == 0;
 }
 
-template <typename T, int D, int B, bool DB, bool A, bool L, int H, bool R>
+template <typename T, int D, int B, bool DB, bool A, bool L, int H, bool R, int W>
 int launch_one(const DecodeParams &p, hipStream_t stream) {
   // Every (sequence, split) item that can exist, times the KV-head groups.
   const int64_t items = (int64_t)p.batch * p.max_splits * (p.hkv / H);
   if (items > 0x7fffffff)
     return set_error(MLR_ERR_UNSUPPORTED, "mlr_paged_decode: %lld work items exceed the grid",
                      (long long)items);
-  decode_mfma<T, D, B, DB, A, L, H, R><<<dim3(static_cast<unsigned>(items)), 64 * kWaves * H,
-                                         0, stream>>>(p);
+  decode_mfma<T, D, B, DB, A, L, H, R, W><<<dim3(static_cast<unsigned>(items)), 64 * W * H,
+                                            0, stream>>>(p);
   return check_launch("mlr_paged_decode(mfma)");
 }
 
 // The three variants of one layout: decode only, with the fused KV write,
 // and with the fused write and rotary embedding (their own instantiations,
 // so the rotary code costs the other two nothing; bf16 only).
-template <typename T, int D, int B, bool DB, bool L, int H = 1>
+template <typename T, int D, int B, bool DB, bool L, int H = 1, int W = kWaves>
 int launch_variant(const DecodeParams &p, hipStream_t stream) {
-  if (p.new_k == nullptr) return launch_one<T, D, B, DB, false, L, H, false>(p, stream);
+  if (p.new_k == nullptr) return launch_one<T, D, B, DB, false, L, H, false, W>(p, stream);
   if constexpr (std::is_same<T, bf16_t>::value) {
-    if (p.inv_freq != nullptr) return launch_one<T, D, B, DB, true, L, H, true>(p, stream);
+    if (p.inv_freq != nullptr) return launch_one<T, D, B, DB, true, L, H, true, W>(p, stream);
   }
-  return launch_one<T, D, B, DB, true, L, H, false>(p, stream);
+  return launch_one<T, D, B, DB, true, L, H, false, W>(p, stream);
 }
 
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
@@ -1240,7 +1244,16 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
   // batches of two), longer splits in double-buffered batches of two; at
   // head_dim 128 one tile per batch. One KV head per workgroup.
   if (p.dtype == MLR_DTYPE_F32) {
+    // A grid that leaves most CUs idle (work items for under a quarter of
+    // them) spreads each split of up to 16 tiles over eight waves, two tiles
+    // each: the split's matrix-core work runs on twice as many SIMDs. At
+    // fp32_decode_b4 (8 work items): 7.04 us per step against 8.32 us with
+    // four waves and 7.66 us with 16 waves of one tile (10-call graphs,
+    // alternating libraries on one box).
+    const int64_t items = (int64_t)p.batch * p.max_splits * p.hkv;
+    const bool spread = cus > 0 && 4 * items <= cus && ceil_div(p.ts, 16) <= 16;
     if (p.d == 64) {
+      if (spread) return launch_variant<float, 64, 2, false, false, 1, 8>(p, stream);
       if (tiles_per_wave <= 4) return launch_variant<float, 64, 4, false, false>(p, stream);
       return launch_variant<float, 64, 2, true, false>(p, stream);
     }
