@@ -89,9 +89,10 @@ CASES = [
     (torch.bfloat16, 40, 2, 64, 16, [77]),                         # generic (G=20)
     (torch.bfloat16, 8, 2, 96, 16, [50, 200]),                     # generic (D=96)
     (torch.float16, 14, 2, 64, 16, [31, 257]),
-    (torch.float32, 14, 2, 64, 16, [1, 255, 600]),                 # FP32 MFMA, merged splits
+    # FP32 MFMA, merged splits; 18 work items: eight waves per KV head
+    (torch.float32, 14, 2, 64, 16, [1, 255, 600]),
     (torch.float32, 28, 4, 128, 16, [33, 700, 2049]),              # FP32 MFMA, D=128
-    (torch.float32, 32, 2, 64, 32, [64, 513, 1]),                  # FP32 MFMA, G=16, BS=32
+    (torch.float32, 32, 2, 64, 32, [64, 513, 1]),                  # G=16, BS=32, eight waves
     (torch.float32, 14, 2, 64, 8, [9, 130]),                       # generic (BS=8)
     (torch.float32, 6, 3, 40, 5, [7, 23]),
     (torch.float64, 4, 2, 16, 4, [3, 19]),
