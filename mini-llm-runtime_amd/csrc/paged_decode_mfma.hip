@@ -732,7 +732,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   st.m = -INFINITY;
   st.l = 0.f;
 
-  // This wave's tiles: w, w + 4, w + 8, ...; block id of the wave's k-th
+  // This wave's tiles: w, w + kW, w + 2 kW, ...; block id of the wave's k-th
   // tile lives in lane (k % 64) of blk_reg (-1: no tile or invalid id).
   const int nk = ntiles > w ? (ntiles - w + kW - 1) / kW : 0;
   auto valid_id = [&](int k, int64_t raw) -> int {
