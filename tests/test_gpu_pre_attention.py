@@ -27,7 +27,7 @@ from oracle.paged_kv_cache import OracleKVCache
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
-SHAPES = [(14, 2, 64), (4, 4, 128), (8, 1, 64), (2, 1, 16)]  # (Hq, Hkv, D)
+SHAPES = [(14, 2, 64), (4, 4, 128), (8, 1, 64), (2, 1, 16), (28, 4, 128)]  # (Hq, Hkv, D)
 THETA = 1_000_000.0
 ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
 
