@@ -29,10 +29,10 @@ Secondary objects: BF16 chunk prefill (8 x 512-token chunks on prefixes
 U[0, 3584]) in TFLOP/s against the 2.5 PFLOP/s bf16 MFMA peak; the decode
 step the serving runtime runs (rotary embedding, KV write and decode in one
 launch) and the same step as two launches (fused pre-attention kernel, then
-decode); the
-read floor of the decode step (config.read_floor: a read-only pass over the
-same K/V rows through the same block tables, mlr_paged_kv_read_floor); the
-8 x 32K decode over rotated pools; the fused pre-attention step; the KV
+decode); the read floor of the decode step (config.read_floor: a read-only
+pass over the same K/V rows through the same block tables,
+mlr_paged_kv_read_floor); the 8 x 32K decode over rotated pools, with its
+own read floor; the fused pre-attention step; the KV
 write on its own (``kv_write``); the FP32 batch-4 decode step; and
 ``serving``, end-to-end continuous-batching steps of a random-init
 Qwen2.5-0.5B-shape model in BF16 (workloads.qwen05b_serving: about 48
