@@ -141,12 +141,13 @@ class Qwen2DecoderLayer(nn.Module):
 
     def forward_decode_batch_with_cache(self, hidden_states, position_ids, kv_cache,
                                         layer_idx, slot_mapping, block_tables,
-                                        context_lens) -> torch.Tensor:
+                                        context_lens, *,
+                                        metadata_checked: bool = False) -> torch.Tensor:
         return self._block(
             hidden_states, lambda h: self.self_attn.forward_decode_batch_with_cache(
                 hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
                 layer_idx=layer_idx, slot_mapping=slot_mapping, block_tables=block_tables,
-                context_lens=context_lens))
+                context_lens=context_lens, metadata_checked=metadata_checked))
 
     def forward_prefill_packed_with_cache(self, hidden_states, position_ids, kv_cache,
                                           layer_idx, slot_mapping, block_tables,
@@ -284,8 +285,12 @@ class TinyQwen2Model(nn.Module):
             raise ValueError("KV cache num_kv_heads must match model num_key_value_heads")
         if kv_cache.head_dim != self.config.head_dim:
             raise ValueError("KV cache head_dim must match model head_dim")
+        # Every layer gets the same metadata tensors: the first layer checks
+        # them (one host sync, before any cache write) and the others do not
+        # repeat the checks.
         return self._run(input_ids, lambda layer, i, h: layer.forward_decode_batch_with_cache(
-            h, position_ids, kv_cache, i, slot_mapping, block_tables, context_lens))
+            h, position_ids, kv_cache, i, slot_mapping, block_tables, context_lens,
+            metadata_checked=i > 0))
 
     def forward_prefill_packed_with_cache(self, input_ids: torch.Tensor,
                                           position_ids: torch.Tensor,

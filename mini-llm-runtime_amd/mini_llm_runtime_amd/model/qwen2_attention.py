@@ -337,8 +337,14 @@ class Qwen2Attention(nn.Module):
                                         position_ids: torch.Tensor, kv_cache: PagedKVCache,
                                         layer_idx: int, slot_mapping: torch.Tensor,
                                         block_tables: torch.Tensor,
-                                        context_lens: torch.Tensor) -> torch.Tensor:
-        """Decode one token per request; context lengths include this token."""
+                                        context_lens: torch.Tensor, *,
+                                        metadata_checked: bool = False) -> torch.Tensor:
+        """Decode one token per request; context lengths include this token.
+
+        metadata_checked: these same position, slot, block-table and length
+        tensors already passed the device-side metadata checks against this
+        cache (the model checks them in its first layer), so they are not
+        checked again; the shape, dtype and device checks still run."""
         if hidden_states.ndim != 3 or hidden_states.shape[1:] != (1, self.hidden_size):
             raise ValueError("hidden_states must have shape [B, 1, hidden_size]")
         batch = hidden_states.shape[0]
@@ -362,8 +368,9 @@ class Qwen2Attention(nn.Module):
             raise ValueError("KV cache must be on the hidden_states device")
         if kv_cache.dtype != hidden_states.dtype:
             raise ValueError("KV cache dtype must match hidden_states dtype")
-        self._check_decode_metadata(kv_cache, position_ids, slot_mapping, block_tables,
-                                    context_lens)
+        if not metadata_checked:
+            self._check_decode_metadata(kv_cache, position_ids, slot_mapping, block_tables,
+                                        context_lens)
         # The metadata checks above are the ones write_slots and the decode
         # would repeat.
         if kpre.qkv_rope_decode_fusable(hidden_states.dtype, kv_cache, self.num_attention_heads):

@@ -278,3 +278,69 @@ def test_qwen05b_serving_fp32_matches_oracle_tokens(device):
     assert all(len(by_id[g["request_id"]].output_token_ids) == len(g["tokens"])
                for g in golden["requests"])  # every golden request ran to its end
     assert compared >= 0.95 * total
+
+
+def _model_decode_case(device):
+    """Three-layer bf16 model and one valid batched-decode step: two requests
+    at contexts 5 and 9 of a 16-block, block-size-4 pool."""
+    cfg_kwargs = dict(TINY, num_hidden_layers=3)
+    _, model, _ = make_model(cfg_kwargs, torch.bfloat16, device, seed=3)
+    cache = PagedKVCache(3, 16, 4, 2, 16, dtype=torch.bfloat16, device=device)
+    cache.k_cache.normal_()
+    cache.v_cache.normal_()
+    tables = torch.tensor([[3, 7, -1], [0, 5, 9]], device=device)
+    ctx = torch.tensor([5, 9], device=device)
+    pos = (ctx - 1).unsqueeze(1)
+    slots = torch.tensor([7 * 4 + 0, 9 * 4 + 0], device=device)
+    ids = torch.tensor([[11], [42]], device=device)
+    return model, cache, dict(input_ids=ids, position_ids=pos, slot_mapping=slots,
+                              block_tables=tables, context_lens=ctx)
+
+
+def test_model_decode_checks_the_step_metadata_once(device, monkeypatch):
+    """The model hands every layer the same metadata tensors: the first layer
+    runs the device-side metadata checks (one host sync) and the others skip
+    them. The result equals the run that checks in every layer, bit for bit."""
+    from mini_llm_runtime_amd.model.qwen2_attention import Qwen2Attention
+
+    model, cache, inputs = _model_decode_case(device)
+    k0, v0 = cache.k_cache.clone(), cache.v_cache.clone()
+    calls = []
+    real = Qwen2Attention._check_decode_metadata
+
+    def counting(*args):
+        calls.append(1)
+        return real(*args)
+
+    monkeypatch.setattr(Qwen2Attention, "_check_decode_metadata", staticmethod(counting))
+    with torch.no_grad():
+        once = model.model.forward_decode_batch_with_cache(kv_cache=cache, **inputs)
+    assert len(calls) == 1
+    k1, v1 = cache.k_cache.clone(), cache.v_cache.clone()
+
+    # Every layer checking, as a caller of the layer API gets.
+    cache.k_cache.copy_(k0)
+    cache.v_cache.copy_(v0)
+    with torch.no_grad():
+        h = model.model.embed_tokens(inputs["input_ids"])
+        for i, layer in enumerate(model.model.layers):
+            h = layer.forward_decode_batch_with_cache(
+                h, inputs["position_ids"], cache, i, inputs["slot_mapping"],
+                inputs["block_tables"], inputs["context_lens"])
+        every = model.model.norm(h)
+    assert len(calls) == 1 + len(model.model.layers)
+    assert torch.equal(once, every)
+    assert torch.equal(cache.k_cache, k1) and torch.equal(cache.v_cache, v1)
+
+
+def test_model_decode_rejects_bad_metadata_before_any_layer_writes(device):
+    """A slot that does not match the block table is refused in the first
+    layer, before any layer's cache is written."""
+    model, cache, inputs = _model_decode_case(device)
+    k0, v0 = cache.k_cache.clone(), cache.v_cache.clone()
+    inputs["slot_mapping"] = torch.tensor([7 * 4 + 1, 9 * 4 + 0], device=device)
+    with pytest.raises(ValueError, match="slot_mapping must match"):
+        with torch.no_grad():
+            model.model.forward_decode_batch_with_cache(kv_cache=cache, **inputs)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k_cache, k0) and torch.equal(cache.v_cache, v0)
