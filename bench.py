@@ -989,7 +989,9 @@ def bench_serving(device, steps=None):
     (workloads.qwen05b_serving): schedule, pack, 24-layer forward on the HIP
     attention kernels with PyTorch GEMMs, sample, update. After the warm-up
     (all 48 initial prompts admitted), each step is timed on the host with a
-    device synchronisation on both sides."""
+    device synchronisation on both sides. Every timed step's logits must be
+    finite (checked after the loop; the merge-failure flag is checked inside
+    each step)."""
     import torch
 
     from mini_llm_runtime_amd import workloads
@@ -1001,17 +1003,22 @@ def bench_serving(device, steps=None):
     times, decode_tokens, prefill_tokens, finished = [], 0, 0, 0
     with torch.no_grad():
         warm = workloads.serving_warm_up(model, scheduler, len(w.initial))
+        finite = []  # per step, read after the timed loop
         for _ in range(steps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             result = run_generation_step(model, scheduler)
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t0)
+            finite.append(torch.isfinite(result.packed_logits).all())
             out = result.scheduler_output
             decode_tokens += len(out.decode_requests)
             prefill_tokens += sum(out.num_scheduled_tokens[r.request_id]
                                   for r in out.prefill_requests)
             finished += len(result.finished_requests)
+        bad = [i for i, ok in enumerate(torch.stack(finite).tolist()) if not ok]
+        if bad:
+            raise RuntimeError(f"{w.name}: non-finite logits at timed steps {bad[:8]}")
         # Host metadata of one step: the device path build_model_batch uses
         # (per-request host work + mlr_build_step_metadata) against the
         # reference-style per-token host construction.
