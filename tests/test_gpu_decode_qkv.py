@@ -258,3 +258,48 @@ def test_qwen05b_b64_served_step_matches_oracle(device):
     pair, _ = _two_launches(qkv_d, inv_freq, two_cache, bt, sl, slots, hq, 0)
     assert torch.equal(one_cache.k_cache, two_cache.k_cache)
     assert torch.equal(got, pair)
+
+
+def _random_served_case(seed):
+    """Shape of a seeded served-step case: head_dim, KV heads, GQA group,
+    batch, context lengths (edge lengths mixed in) and split size."""
+    gen = torch.Generator().manual_seed(9100 + seed)
+
+    def pick(values):
+        return values[int(torch.randint(len(values), (1,), generator=gen))]
+
+    d = pick([64, 64, 128])
+    hkv = pick([1, 2, 2, 4])
+    group = pick([1, 2, 4, 7, 8, 16])
+    batch = int(torch.randint(1, 25, (1,), generator=gen))
+    lens = torch.randint(1, 3001, (batch,), generator=gen).tolist()
+    edges = [1, 15, 16, 17, 319, 320, 321, 640]
+    for i in range(0, batch, 3):
+        lens[i] = pick(edges)
+    return d, hkv * group, hkv, lens, pick([0, 0, 64, 128, 176, 320])
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_served_steps_equal_the_two_launches(device, seed):
+    """Seeded random shapes of the one-launch served step: equal to
+    mlr_qkv_rope_write followed by the decode bit for bit (output and cache),
+    and within 2e-2 of the oracle's decode."""
+    d, hq, hkv, lens, ts = _random_served_case(seed)
+    shape = f"seed {seed}: d={d} hq={hq} hkv={hkv} batch={len(lens)} ts={ts} lens={lens}"
+    qkv, kc, vc, bt, sl, slots, tables = _case(hq, hkv, d, lens, seed=500 + seed)
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
+    qkv, bt, sl, slots = (t.to(device) for t in (qkv, bt, sl, slots))
+
+    two_cache = _cache(kc, vc, device)
+    want, q = _two_launches(qkv, inv_freq, two_cache, bt, sl, slots, hq, ts)
+    one_cache = _cache(kc, vc, device)
+    got = kpre.qkv_rope_decode(qkv, inv_freq, one_cache, 0, slots, bt, sl, hq,
+                               tokens_per_split=ts)
+    assert torch.equal(one_cache.k_cache, two_cache.k_cache), shape
+    assert torch.equal(one_cache.v_cache, two_cache.v_cache), shape
+    assert torch.equal(got, want), shape
+
+    k, v = two_cache.get_layer_cache(0)
+    oracle = opa.decode_batch_loop(q.cpu(), k.cpu(), v.cpu(), tables, lens, BS)
+    assert torch.isfinite(got).all(), shape
+    assert (got.double().cpu() - oracle.double()).abs().max().item() <= 2e-2, shape
