@@ -790,6 +790,82 @@ def bench_decode_32k(device, reps=4, calls_per_graph=6):
             "frac_of_hbm_peak_best": round(nbytes / best_us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
+# The reference's published split-KV decode latencies (one request, Triton,
+# fp16, RTX 5070 Ti Laptop GPU): benchmarks/results/paged_attention/
+# seq_scaling.csv:2-7, split_kernel_ms.
+REFERENCE_SPLIT_KV_US = {512: 18.21, 1024: 22.30, 2048: 31.94, 4096: 48.80, 8192: 83.30,
+                         16384: 169.70}
+
+
+def bench_reference_shapes(device, reps=3):
+    """The reference's own decode benchmark shape
+    (benchmarks/benchmark_paged_attention.py:206-210: one request, 32 q / 8 KV
+    heads, head_dim 128, block 16) at the sequence lengths it publishes, on
+    this library's decode (mlr_paged_decode, default split), in bf16 and in
+    fp16 (the reference's default dtype), both on the matrix-core kernel. Each call reads one of enough copies of the K/V pool to exceed
+    the 256 MB MALL, so every call reads HBM, as the reference's do_bench
+    flushes its cache between calls."""
+    import math
+
+    import torch
+
+    from mini_llm_runtime_amd.kernels import paged_attention as kpa
+
+    hq, hkv, d, bs = 32, 8, 128, 16
+    stream = torch.cuda.Stream(device)
+    out = {}
+    for dtype, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        by_len = {}
+        for seq in REFERENCE_SPLIT_KV_US:
+            nb = seq // bs
+            gen = torch.Generator().manual_seed(seq)
+            pool_bytes = 2 * nb * bs * hkv * d * 2
+            copies = min(256, max(2, math.ceil(600e6 / pool_bytes)))
+            k = torch.randn(nb, bs, hkv, d, generator=gen).to(device=device, dtype=dtype)
+            v = torch.randn(nb, bs, hkv, d, generator=gen).to(device=device, dtype=dtype)
+            pools = [(k.clone(), v.clone()) for _ in range(copies)]
+            del k, v
+            q = torch.randn(1, hq, d, generator=gen).to(device=device, dtype=dtype)
+            bt = torch.randperm(nb, generator=gen).view(1, nb).to(device)
+            ctx = torch.tensor([seq], device=device)
+            res = torch.empty_like(q)
+            ws = torch.zeros(kpa.decode_workspace_bytes(1, hq, d, seq, dtype),
+                             dtype=torch.uint8, device=device)
+
+            def call(i):
+                kc, vc = pools[i % copies]
+                kpa.paged_decode_launch(q, kc, vc, bt, ctx, res, workspace=ws)
+
+            stream.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(stream):
+                for i in range(copies):
+                    call(i)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(copies):
+                    call(i)
+            warm_graph(g, stream, seconds=0.1)
+            us = timed_graph(g, reps, stream) / (reps * copies) * 1e6
+            check_decode_outputs(kpa, ws, res, stream, f"reference shape {name} {seq}")
+            kv_bytes = 2 * seq * hkv * d * 2
+            by_len[str(seq)] = {"us": round(us, 2), "GBps": round(kv_bytes / us / 1e3, 1),
+                                "pools_rotated": copies}
+            del pools, g
+            torch.cuda.empty_cache()
+        out[name] = by_len
+    return {
+        "shape": "one request, 32 q / 8 KV heads, head_dim 128, block 16 (the reference's "
+                 "benchmark_paged_attention.py defaults)",
+        "kernels": {"bf16": "matrix-core split-KV decode, merged in one launch",
+                    "fp16": "matrix-core split-KV decode, merged in one launch"},
+        "us_by_seq_len": out,
+        "reference_published_us": {str(k): v for k, v in REFERENCE_SPLIT_KV_US.items()},
+        "reference_published_on": "RTX 5070 Ti Laptop GPU, Triton split-KV kernel, fp16 "
+                                  "(seq_scaling.csv split_kernel_ms; its merge pass is extra)",
+    }
+
+
 def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=100):
     """The CUDA accumulator extension's contract (p [B, 64], v [B, 64, 256],
     FP32) on mlr_pa_accumulate at the reference test's largest batch."""
@@ -1242,6 +1318,7 @@ def main():
     line["decode_32k"] = bench_decode_32k(device)
     line["decode_32k"]["traffic"] = traffic.get("decode_32k_bytes") if traffic else None
     line["accumulator"] = bench_accumulator(device)
+    line["reference_shapes"] = bench_reference_shapes(device)
     if not args.no_serving:
         line["serving"] = bench_serving(device)
     print(json.dumps(line), flush=True)

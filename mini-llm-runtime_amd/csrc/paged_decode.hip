@@ -14,8 +14,8 @@
 // scale (rounded again), then an FP32 softmax over positions t < seq_len;
 // positions past seq_len and padded block-table entries never contribute.
 //
-// bf16 and FP32 inputs with head_dim 64 or 128, at most 16 query heads per KV
-// head and block_size a multiple of 16 take the matrix-core kernel in
+// bf16, fp16 and FP32 inputs with head_dim 64 or 128, at most 16 query heads
+// per KV head and block_size a multiple of 16 take the matrix-core kernel in
 // paged_decode_mfma.hip (one launch, splits merged in it); everything else
 // takes the generic kernels below.
 #include <algorithm>
@@ -278,7 +278,8 @@ int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_contex
     while (ts < 256 && ts * 8 < max_context) ts *= 2;
     return ts;
   }
-  if (dtype == MLR_DTYPE_BF16 && head_dim == 64 && max_context <= 16 * kLdsSplit64)
+  if ((dtype == MLR_DTYPE_BF16 || dtype == MLR_DTYPE_F16) && head_dim == 64 &&
+      max_context <= 16 * kLdsSplit64)
     return kLdsSplit64;
   const int64_t per16 = ceil_div(max_context, 16);
   return per16 <= 256 ? 256 : ceil_div(per16, 256) * 256;

@@ -1,4 +1,4 @@
-// bf16 and FP32 split-KV paged decode on gfx950 matrix cores, in one launch.
+// bf16, fp16 and FP32 split-KV paged decode on gfx950 matrix cores, in one launch.
 //
 // One workgroup of four wavefronts per (live split, KV head), or of eight per
 // (live split, pair of KV heads), four for each head (FP32 grids that leave
@@ -50,6 +50,11 @@
 // to bf16 again: kernels/reference/paged_attention.py:246-247) before the
 // FP32 softmax (:251).
 //
+// fp16 inputs take the bf16 layout with v_mfma_f32_16x16x32_f16 and
+// v_mfma_f32_16x16x16_f16, and round scores and probabilities to fp16 where
+// the bf16 tile rounds to bf16 (the reference's fp16 matmul, scale and
+// probs.to(v.dtype)).
+//
 // FP32 inputs take the same kernel with v_mfma_f32_16x16x4_f32 in place of
 // the bf16 instructions (compute_tile for Tile<float, D>): its 16x16
 // accumulator has the bf16 tiles' layout, so the softmax, the merges, the
@@ -61,6 +66,8 @@ namespace mlr {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -83,6 +90,7 @@ template <int D> struct TileTraits<bf16_t, D> {
   using VT = typename VRow<D>::type;
   using S = uint16_t;  // storage element
 };
+template <int D> struct TileTraits<f16_t, D> : TileTraits<bf16_t, D> {};
 template <> struct TileTraits<float, 64> {
   static constexpr int kKChunks = 4;
   using VT = uint4;
@@ -115,6 +123,53 @@ __device__ __forceinline__ float bf16_elem(const uint4 &v, int e) {
   const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
   return bf16_bits_to_float((e & 1) ? (w >> 16) : (w & 0xffffu));
 }
+
+// a and b rounded to fp16 (nearest even) and back to FP32.
+__device__ __forceinline__ void f16_round2(float &a, float &b) {
+  typedef float f32x2_v __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+  const f16x2_v h = __builtin_convertvector(f32x2_v{a, b}, f16x2_v);
+  a = static_cast<float>(h[0]);
+  b = static_cast<float>(h[1]);
+}
+
+__device__ __forceinline__ uint32_t f16_pack2(float lo, float hi) {
+  const _Float16 a = static_cast<_Float16>(lo);
+  const _Float16 b = static_cast<_Float16>(hi);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+// The 16-bit element types on the matrix cores: the reference computes q.k,
+// the scale and the probabilities in the input dtype, so the tile rounds
+// them to that dtype (nearest even), and the MFMAs take that dtype's
+// operands with FP32 accumulation.
+template <typename T> struct Half16;
+template <> struct Half16<bf16_t> {
+  using v8 = bf16x8_t;
+  __device__ static void round2(float &a, float &b) { bf16_round2(a, b); }
+  __device__ static uint32_t pack2(float lo, float hi) { return bf16_pack2(lo, hi); }
+  __device__ static f32x4_t qk(uint4 k, v8 q, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, k), q, c, 0, 0, 0);
+  }
+  __device__ static f32x4_t pv(s16x4_t v, s16x4_t p, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v, p, c, 0, 0, 0);
+  }
+  __device__ static uint16_t store(float x) { return float_to_bf16_bits(x); }
+};
+template <> struct Half16<f16_t> {
+  using v8 = f16x8_t;
+  __device__ static void round2(float &a, float &b) { f16_round2(a, b); }
+  __device__ static uint32_t pack2(float lo, float hi) { return f16_pack2(lo, hi); }
+  __device__ static f32x4_t qk(uint4 k, v8 q, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, k), q, c, 0, 0, 0);
+  }
+  __device__ static f32x4_t pv(s16x4_t v, s16x4_t p, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, v),
+                                                 __builtin_bit_cast(f16x4_t, p), c, 0, 0, 0);
+  }
+  __device__ static uint16_t store(float x) { return float_to_f16_bits(x); }
+};
 
 // Rotary embedding of one (x[i], x[i + d/2]) pair in bf16 as the reference's
 // apply_rotary_pos_emb computes it (model/qwen2.py:125-209), operation by
@@ -307,7 +362,8 @@ __device__ __forceinline__ void copy_tile_to_lds(unsigned char *dst, const uint1
 
 // The register fragments of a tile landed by copy_tile_to_lds, in the layout
 // load_tile gives them (head_dim 64).
-__device__ __forceinline__ void read_tile_from_lds(Tile<bf16_t, 64> &t, const unsigned char *src,
+template <typename T>
+__device__ __forceinline__ void read_tile_from_lds(Tile<T, 64> &t, const unsigned char *src,
                                                    int blk, int rel, int m16, int g) {
   t.blk = blk;
   t.rel = rel;
@@ -348,11 +404,13 @@ __device__ __forceinline__ void softmax_update(DecodeState<D> &st, const float (
 // and V rows, staged in LDS (new_row: K row then V row), in place of what was
 // read from the cache; the substitution is a per-lane select at compute time,
 // so it never waits on the tile's loads and holds no registers before.
-template <int D, bool kAppend>
-__device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<bf16_t, D> &t,
-                                             const bf16x8_t *qf, float scale,
+// bf16 and fp16 (Half16 gives the dtype's rounding and MFMAs).
+template <int D, bool kAppend, typename T>
+__device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<T, D> &t,
+                                             const typename Half16<T>::v8 *qf, float scale,
                                              int live, int g, int m16,
                                              const uint16_t *new_row) {
+  using H = Half16<T>;
   constexpr int QK = D / 32, VC = D / 16;
   using VT = typename VRow<D>::type;
   if (t.blk < 0) return;  // absent tile or invalid block id: no keys (uniform)
@@ -372,16 +430,14 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<bf16_t, D>
 
   f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < QK; ++j)
-    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, t.k[j]),
-                                                qf[j], s, 0, 0, 0);
+  for (int j = 0; j < QK; ++j) s = H::qk(t.k[j], qf[j], s);
   float r[4] = {s[0], s[1], s[2], s[3]};
-  bf16_round2(r[0], r[1]);
-  bf16_round2(r[2], r[3]);
+  H::round2(r[0], r[1]);
+  H::round2(r[2], r[3]);
 #pragma unroll
   for (int i = 0; i < 4; ++i) r[i] *= scale;
-  bf16_round2(r[0], r[1]);
-  bf16_round2(r[2], r[3]);
+  H::round2(r[0], r[1]);
+  H::round2(r[2], r[3]);
   float x[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) x[i] = (4 * g + i < lim) ? r[i] * kLog2e : -INFINITY;
@@ -394,7 +450,7 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<bf16_t, D>
       if (4 * g + i >= lim) t.v[i] = VT{};
   }
   const s16x4_t pb = __builtin_bit_cast(
-      s16x4_t, make_uint2(bf16_pack2(pr[0], pr[1]), bf16_pack2(pr[2], pr[3])));
+      s16x4_t, make_uint2(H::pack2(pr[0], pr[1]), H::pack2(pr[2], pr[3])));
 #pragma unroll
   for (int n = 0; n < VC; ++n) {
     const int c = n >> 1, h = n & 1;
@@ -403,7 +459,7 @@ __device__ __forceinline__ void compute_tile(DecodeState<D> &st, Tile<bf16_t, D>
     const uint32_t lo = __builtin_amdgcn_perm(vword<D>(t.v[1], c), vword<D>(t.v[0], c), sel);
     const uint32_t hi = __builtin_amdgcn_perm(vword<D>(t.v[3], c), vword<D>(t.v[2], c), sel);
     const s16x4_t va = __builtin_bit_cast(s16x4_t, make_uint2(lo, hi));
-    st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, st.acc[n], 0, 0, 0);
+    st.acc[n] = H::pv(va, pb, st.acc[n]);
   }
 }
 
@@ -585,8 +641,10 @@ template <typename T, int D, int kBatch, bool kDouble, bool kAppend, bool kLds, 
 __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkItem &it,
                                             int kvh_base) {
   constexpr bool kF32 = std::is_same<T, float>::value;
-  static_assert(kF32 || std::is_same<T, bf16_t>::value, "bf16 or FP32 elements");
-  static_assert(!kF32 || (!kLds && !kRope), "the LDS tile and the rotary embedding are bf16");
+  constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
+  static_assert(kF32 || kBf16 || std::is_same<T, f16_t>::value, "bf16, fp16 or FP32 elements");
+  static_assert(!kF32 || !kLds, "the LDS tile is for 16-bit elements");
+  static_assert(!kRope || kBf16, "the rotary embedding is bf16");
   using S = typename TileTraits<T, D>::S;  // storage element
   constexpr int QK = TileTraits<T, D>::kKChunks;
   constexpr int kSize = static_cast<int>(sizeof(T));
@@ -682,7 +740,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
 
   // Q^T as the B operand: lane l holds Q[head l%16][4kE j + kE g .. +kE)
   // (bf16: 32j + 8g; FP32: 16j + 4g), the dims of its K chunks.
-  using QF = typename std::conditional<kF32, f32x4_t, bf16x8_t>::type;
+  using QF = typename std::conditional<kF32, f32x4_t,
+                                       typename std::conditional<kBf16, bf16x8_t, f16x8_t>::type>::type;
   QF qf[QK];
 #pragma unroll
   for (int j = 0; j < QK; ++j) qf[j] = __builtin_bit_cast(QF, qraw[j]);
@@ -693,7 +752,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // (no instruction) keeps the compiler from moving the other lanes' reads
   // above those writes.
   auto rotate_q = [&]() {
-    if constexpr (!kF32) {
+    if constexpr (kBf16) {
     if (lane < D / 2) {
       // sincosf shares one argument reduction between the two; its results
       // are those of cosf and sinf.
@@ -855,7 +914,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
     // fifth in this wave's LDS slot, all issued up front, so that one
     // workgroup keeps 80 KB in flight and the splits of a batch like 64
     // sequences of up to 4K tokens fit the GPU in one generation.
-    static_assert(D == 64 && kBatch == 4 && !kF32, "LDS landing is laid out for bf16 head_dim 64");
+    static_assert(D == 64 && kBatch == 4 && !kF32,
+                  "LDS landing is laid out for 16-bit elements at head_dim 64");
     __shared__ __align__(16) unsigned char lds_tiles[kW * kH][kLdsTileBytes];
     Tile<T, D> buf[kBatch];
     issue(buf, 0);
@@ -915,7 +975,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   S *out = static_cast<S *>(p.out);
   auto store_out = [&](float x) -> S {
     if constexpr (kF32) return x;
-    else return float_to_bf16_bits(x);
+    else return Half16<T>::store(x);
   };
   // The workgroup's partial rows: (m, l) pairs and acc rows for its heads h
   // and splits s at row h * split_stride + s, under buffer resources of their
@@ -1194,7 +1254,7 @@ __global__ __launch_bounds__(64 * kW * kH) void decode_mfma(DecodeParams p) {
 
 bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
                           int64_t block_size) {
-  return (dtype == MLR_DTYPE_BF16 || dtype == MLR_DTYPE_F32) &&
+  return (dtype == MLR_DTYPE_BF16 || dtype == MLR_DTYPE_F16 || dtype == MLR_DTYPE_F32) &&
          (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 16 &&
          block_size % 16 == 0;
 }
@@ -1221,6 +1281,27 @@ int launch_variant(const DecodeParams &p, hipStream_t stream) {
     if (p.inv_freq != nullptr) return launch_one<T, D, B, DB, true, L, H, true, W>(p, stream);
   }
   return launch_one<T, D, B, DB, true, L, H, false, W>(p, stream);
+}
+
+// bf16 and fp16 instantiations: head_dim x (one load batch | + LDS tile |
+// double-buffered) x KV heads per workgroup x variant (the rotary variant is
+// bf16 only).
+template <typename T>
+int launch_16bit(const DecodeParams &p, int tiles_per_wave, bool pairs, hipStream_t stream) {
+  if (p.d == 64) {
+    if (tiles_per_wave <= 4) return launch_variant<T, 64, 4, false, false>(p, stream);
+    if (p.ts == kLdsSplit64) {
+      if (pairs) return launch_variant<T, 64, 4, false, true, 2>(p, stream);
+      return launch_variant<T, 64, 4, false, true>(p, stream);
+    }
+    return launch_variant<T, 64, 4, true, false>(p, stream);
+  }
+  if (pairs) {
+    if (tiles_per_wave <= 2) return launch_variant<T, 128, 2, false, false, 2>(p, stream);
+    return launch_variant<T, 128, 2, true, false, 2>(p, stream);
+  }
+  if (tiles_per_wave <= 2) return launch_variant<T, 128, 2, false, false>(p, stream);
+  return launch_variant<T, 128, 2, true, false>(p, stream);
 }
 
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
@@ -1260,22 +1341,8 @@ int launch_decode_mfma(const DecodeParams &p, hipStream_t stream) {
     if (tiles_per_wave <= 1) return launch_variant<float, 128, 1, false, false>(p, stream);
     return launch_variant<float, 128, 1, true, false>(p, stream);
   }
-  // bf16 instantiations: head_dim x (one load batch | + LDS tile |
-  // double-buffered) x KV heads per workgroup x variant.
-  if (p.d == 64) {
-    if (tiles_per_wave <= 4) return launch_variant<bf16_t, 64, 4, false, false>(p, stream);
-    if (p.ts == kLdsSplit64) {
-      if (pairs) return launch_variant<bf16_t, 64, 4, false, true, 2>(p, stream);
-      return launch_variant<bf16_t, 64, 4, false, true>(p, stream);
-    }
-    return launch_variant<bf16_t, 64, 4, true, false>(p, stream);
-  }
-  if (pairs) {
-    if (tiles_per_wave <= 2) return launch_variant<bf16_t, 128, 2, false, false, 2>(p, stream);
-    return launch_variant<bf16_t, 128, 2, true, false, 2>(p, stream);
-  }
-  if (tiles_per_wave <= 2) return launch_variant<bf16_t, 128, 2, false, false>(p, stream);
-  return launch_variant<bf16_t, 128, 2, true, false>(p, stream);
+  if (p.dtype == MLR_DTYPE_F16) return launch_16bit<f16_t>(p, tiles_per_wave, pairs, stream);
+  return launch_16bit<bf16_t>(p, tiles_per_wave, pairs, stream);
 }
 
 }  // namespace mlr

@@ -88,7 +88,12 @@ CASES = [
     (torch.bfloat16, 14, 2, 64, 8, [9, 130]),                      # generic (BS=8)
     (torch.bfloat16, 40, 2, 64, 16, [77]),                         # generic (G=20)
     (torch.bfloat16, 8, 2, 96, 16, [50, 200]),                     # generic (D=96)
-    (torch.float16, 14, 2, 64, 16, [31, 257]),
+    (torch.float16, 14, 2, 64, 16, [31, 257, 1000]),               # fp16 MFMA, LDS tile
+    (torch.float16, 16, 2, 64, 16, [100, 321, 640, 2000]),         # fp16 MFMA, KV pair
+    (torch.float16, 28, 4, 128, 16, [33, 700, 2049]),              # fp16 MFMA, D=128
+    (torch.float16, 8, 8, 64, 16, [5, 100]),                       # fp16 MFMA, G=1
+    (torch.float16, 32, 2, 64, 32, [64, 513]),                     # fp16 MFMA, G=16, BS=32
+    (torch.float16, 14, 2, 64, 8, [9, 130]),                       # generic (BS=8)
     # FP32 MFMA, merged splits; 18 work items: eight waves per KV head
     (torch.float32, 14, 2, 64, 16, [1, 255, 600]),
     (torch.float32, 28, 4, 128, 16, [33, 700, 2049]),              # FP32 MFMA, D=128
@@ -127,6 +132,8 @@ def test_split_size_does_not_change_the_result(device, tokens_per_split):
     (torch.bfloat16, [1, 16, 17, 300, 1000, 257], 0),     # fused in the MFMA kernel
     (torch.bfloat16, [33, 64, 500], 64),
     (torch.bfloat16, [300, 384, 770, 5], 384),              # new token in an LDS tile
+    (torch.float16, [1, 16, 17, 300, 1000, 257], 0),      # fp16, fused in the MFMA kernel
+    (torch.float16, [33, 64, 500, 2000], 128),
     (torch.float32, [5, 255, 256], 0),                     # fused in the FP32 MFMA kernel
     (torch.float32, [300, 384, 770, 5, 1000, 2049], 64),   # FP32, splits merged in-launch
 ])
