@@ -69,7 +69,8 @@ int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_contex
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype);
 
-// bf16 or FP32, head_dim 64/128, GQA group <= 16 and block_size a multiple of 16.
+// bf16, fp16 or FP32, head_dim 64/128, GQA group <= 16 and block_size a
+// multiple of 16.
 bool decode_mfma_eligible(int dtype, int64_t head_dim, int64_t group,
                           int64_t block_size);
 int launch_decode_mfma(const DecodeParams &p, hipStream_t stream);

@@ -285,6 +285,26 @@ int64_t default_tokens_per_split(bool mfma, int64_t head_dim, int64_t max_contex
   return per16 <= 256 ? 256 : ceil_div(per16, 256) * 256;
 }
 
+// bf16/fp16 matrix-core kernel when the default split gives fewer work items
+// (sequence, KV head, split) than the GPU has CUs: a sixteenth of the context,
+// in whole 64-token steps of at least 64 tokens, up to 512-token splits; then
+// 512-token splits up to 32 of them; then 32 splits. Measured on one request,
+// 32 q / 8 KV heads, head_dim 128 (graphs, every call from HBM): 512 tokens
+// 7.9 us against 10.0 us with two 256-token splits, 2048 tokens 9.4 against
+// 10.9 us, 16K 21.5 against 22.8 us, 32K 33.8 against 37.9 us; 28/4 heads at
+// 32K 28.8 against 36.6 us; 14/2 heads, head_dim 64, at 512 tokens 6.9
+// against 8.6 us (two 320-token splits). Splits of one tile per wave (64
+// tokens) past 512 tokens, or more than 32 splits, were slower: the merge
+// then reads more chunks than the extra waves save. At most 32 splits, and
+// never more than the generic kernel's default split count rounded up to the
+// 16-row padding, so mlr_paged_decode_workspace_size covers it.
+static int64_t sparse_tokens_per_split(int64_t max_context) {
+  const int64_t per16 = ceil_div(ceil_div(max_context, 16), 64) * 64;
+  if (per16 <= 512) return per16 < 64 ? 64 : per16;
+  const int64_t per32 = ceil_div(ceil_div(max_context, 32), 16) * 16;
+  return per32 < 512 ? 512 : per32;
+}
+
 DecodeWorkspace decode_workspace_layout(int64_t batch, int64_t hq, int64_t d,
                                         int64_t max_splits, int dtype) {
   DecodeWorkspace w;
@@ -373,6 +393,11 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
       decode_mfma_eligible(dtype, head_dim, num_q_heads / num_kv_heads, block_size);
   int64_t ts = tokens_per_split > 0 ? tokens_per_split
                                     : default_tokens_per_split(mfma, head_dim, max_context, dtype);
+  if (tokens_per_split <= 0 && mfma && (dtype == MLR_DTYPE_BF16 || dtype == MLR_DTYPE_F16)) {
+    const int cus = current_device_cus();
+    if (cus > 0 && batch * num_kv_heads * ceil_div(max_context, ts) < cus)
+      ts = sparse_tokens_per_split(max_context);
+  }
   if (!mfma) {
     MLR_REQUIRE(ts <= kGenMaxSplit,
                 "mlr_paged_decode: tokens_per_split %lld exceeds %d for this "
