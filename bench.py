@@ -866,6 +866,126 @@ def bench_reference_shapes(device, reps=3):
     }
 
 
+# The reference's published batched decode steps of the whole model
+# (benchmarks/benchmark_decode_runtime.py, Qwen2.5-0.5B, block 16, median of
+# 50 synchronised wall-clock samples after 10 warm-up calls, RTX 5070 Ti
+# Laptop GPU): (dtype, batch, context, ragged) -> ms per step.
+# benchmarks/results/decode_runtime_qwen25_bf16_b8_s512_ragged_reduced_default.csv:3,
+# decode_runtime_qwen25_bf16_b16_s128_reduced_default.csv:3,
+# decode_runtime_qwen25_bf16_s32_128_512.csv:21 (its JSON: dtype float32).
+REFERENCE_DECODE_RUNTIME_MS = {("bf16", 8, 512, True): 41.98, ("bf16", 16, 128, False): 40.32,
+                               ("fp32", 16, 128, False): 45.30}
+
+
+def bench_decode_runtime(device, warmup=10, samples=50):
+    """One batched decode step of the whole 24-layer model
+    (TinyQwen2ForCausalLM.forward_decode_batch_with_cache: embedding, every
+    layer's QKV GEMM, rotation, KV write and paged decode, MLP, final norm and
+    LM head) at the reference's decode-benchmark cases, timed as it times
+    them: host wall clock with a device synchronisation on both sides, median
+    of `samples` calls after `warmup`. Ragged lengths follow the reference's
+    formula, max(2, L/2 + (L - L/2)(i + 1)/B) for request i
+    (benchmark_decode_runtime.py:202-203). Each request's prompt (context - 1
+    random token ids) is prefilled through the model first; the timed step
+    writes the next token of every request at position context - 1, the same
+    slots on every call. Random-init weights (no checkpoint here); the step's
+    time does not depend on their values. Each case is timed twice: the eager
+    forward (as the reference runs it) and the same step replayed from a HIP
+    graph (runtime/decode_graphs.py: the metadata checks with one host sync,
+    the input copies and the replay, inside the timed call). Every timed
+    call's logits must be finite."""
+    import math
+
+    import torch
+
+    from mini_llm_runtime_amd.model.qwen2 import TinyQwen2Config, TinyQwen2ForCausalLM
+    from mini_llm_runtime_amd.runtime.decode_graphs import DecodeGraphs
+    from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
+    from mini_llm_runtime_amd.workloads import QWEN05B_CONFIG
+
+    cfg = TinyQwen2Config(**QWEN05B_CONFIG)
+    bs = 16
+    out = {}
+    models = {}
+    with torch.no_grad():
+        for (name, batch, ctx, ragged), ref_ms in REFERENCE_DECODE_RUNTIME_MS.items():
+            dtype = torch.bfloat16 if name == "bf16" else torch.float32
+            if name not in models:
+                models.clear()
+                torch.manual_seed(0)
+                models[name] = TinyQwen2ForCausalLM(cfg).to(device=device, dtype=dtype).eval()
+            model = models[name]
+            lengths = ([max(2, ctx // 2 + (ctx - ctx // 2) * (i + 1) // batch)
+                        for i in range(batch)] if ragged else [ctx] * batch)
+            cache = PagedKVCache(cfg.num_hidden_layers, sum(math.ceil(n / bs) for n in lengths),
+                                 bs, cfg.num_key_value_heads, cfg.head_dim, dtype=dtype,
+                                 device=device)
+            gen = torch.Generator().manual_seed(1000 * batch + ctx)
+            pending = []
+            for i, n in enumerate(lengths):
+                cache.add_sequence(i)
+                assert cache.reserve_tokens(i, n)
+                table = cache.block_tables[i]
+                ids = torch.randint(10, 1000, (1, n - 1), generator=gen).to(device)
+                pos = torch.arange(n - 1, device=device)
+                slots = torch.tensor([table[t // bs] * bs + t % bs for t in range(n - 1)],
+                                     device=device)
+                logits = model.forward_prefill_with_cache(ids, pos[None, :], cache, slots)
+                pending.append(int(logits[0, -1].argmax()))
+            tables = [cache.block_tables[i] for i in range(batch)]
+            width = max(map(len, tables))
+            block_tables = torch.tensor([t + [-1] * (width - len(t)) for t in tables],
+                                        device=device)
+            contexts = torch.tensor(lengths, device=device)
+            positions = (contexts - 1)[:, None]
+            ids = torch.tensor(pending, device=device)[:, None]
+            slots = torch.tensor([tables[i][(n - 1) // bs] * bs + (n - 1) % bs
+                                  for i, n in enumerate(lengths)], device=device)
+
+            graphs = DecodeGraphs(model, cache, max_blocks_per_seq=width)
+
+            def eager():
+                return model.forward_decode_batch_with_cache(ids, positions, cache, slots,
+                                                             block_tables, contexts)[:, 0]
+
+            def replayed():
+                return graphs(ids, positions, slots, block_tables, contexts)[:, 0]
+
+            row = {"contexts": f"{min(lengths)}..{max(lengths)}",
+                   "reference_published_ms": ref_ms}
+            for mode, step in (("eager", eager), ("graph", replayed)):
+                for _ in range(warmup):
+                    step()
+                times, finite = [], []
+                for _ in range(samples):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    logits = step()
+                    torch.cuda.synchronize()
+                    times.append((time.perf_counter() - t0) * 1e3)
+                    finite.append(torch.isfinite(logits).all())
+                if not bool(torch.stack(finite).all()):
+                    raise RuntimeError(f"decode runtime {name} B={batch} {mode}: "
+                                       "non-finite logits")
+                med = statistics.median(times)
+                row[mode] = {"median_ms": round(med, 3),
+                             "p95_ms": round(sorted(times)[int(0.95 * (len(times) - 1))], 3),
+                             "tokens_per_s": round(batch / med * 1e3, 1),
+                             "reference_over_this": round(ref_ms / med, 2)}
+            out[f"{name}_b{batch}_ctx{ctx}" + ("_ragged" if ragged else "")] = row
+            del graphs, cache
+    return {
+        "what": ("TinyQwen2ForCausalLM.forward_decode_batch_with_cache, Qwen2.5-0.5B "
+                 "architecture (random-init weights), block 16, one batched decode step; "
+                 "eager, and replayed from a HIP graph (DecodeGraphs)"),
+        "timing": (f"host wall clock with device synchronisation on both sides, median of "
+                   f"{samples} calls after {warmup} warm-up calls (the reference's method)"),
+        "reference_published_on": ("RTX 5070 Ti Laptop GPU, Qwen2.5-0.5B checkpoint "
+                                   "(benchmarks/results/decode_runtime_qwen25_*.csv)"),
+        "cases": out,
+    }
+
+
 def bench_accumulator(device, batch=1024, reps=4, calls_per_graph=100):
     """The CUDA accumulator extension's contract (p [B, 64], v [B, 64, 256],
     FP32) on mlr_pa_accumulate at the reference test's largest batch."""
@@ -1060,14 +1180,18 @@ def cpu_baseline_prefill(wl, budget):
     }
 
 
-def bench_serving(device, steps=None):
+def bench_serving(device, steps=None, decode_graphs=False):
     """End-to-end continuous-batching steps at Qwen2.5-0.5B shape in BF16
     (workloads.qwen05b_serving): schedule, pack, 24-layer forward on the HIP
     attention kernels with PyTorch GEMMs, sample, update. After the warm-up
     (all 48 initial prompts admitted), each step is timed on the host with a
     device synchronisation on both sides. Every timed step's logits must be
     finite (checked after the loop; the merge-failure flag is checked inside
-    each step)."""
+    each step). decode_graphs: each step's decodes replay the batched decode
+    forward from a HIP graph per batch size (runtime/decode_graphs.py), block
+    tables padded to the workload's longest request; the graphs of every batch
+    size up to the scheduler's max_num_seqs are recorded before the warm-up
+    (their recording time is reported, outside the steps)."""
     import torch
 
     from mini_llm_runtime_amd import workloads
@@ -1075,15 +1199,27 @@ def bench_serving(device, steps=None):
 
     w = workloads.qwen05b_serving()
     steps = steps or w.steps
-    _, model, _, scheduler, _ = workloads.build_serving(w, device, torch.bfloat16)
+    _, model, cache, scheduler, _ = workloads.build_serving(w, device, torch.bfloat16)
+    graphs = None
+    if decode_graphs:
+        from mini_llm_runtime_amd.runtime.decode_graphs import DecodeGraphs
+
+        longest = max(len(p) + m for p, m in w.initial + w.arrivals)
+        graphs = DecodeGraphs(model, cache, max_blocks_per_seq=-(-longest // w.block_size))
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            graphs.record(range(1, w.max_num_seqs + 1))
+        torch.cuda.synchronize()
+        record_s = time.perf_counter() - t0
     times, decode_tokens, prefill_tokens, finished = [], 0, 0, 0
     with torch.no_grad():
-        warm = workloads.serving_warm_up(model, scheduler, len(w.initial))
+        warm = workloads.serving_warm_up(model, scheduler, len(w.initial),
+                                         decode_graphs=graphs)
         finite = []  # per step, read after the timed loop
         for _ in range(steps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            result = run_generation_step(model, scheduler)
+            result = run_generation_step(model, scheduler, decode_graphs=graphs)
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t0)
             finite.append(torch.isfinite(result.packed_logits).all())
@@ -1128,6 +1264,10 @@ def bench_serving(device, steps=None):
         "tokens_per_s": round((decode_tokens + prefill_tokens) / total, 1),
         "decode_tokens_per_s": round(decode_tokens / total, 1),
         "requests_finished": finished,
+        "decode_graphs": (None if graphs is None else
+                          {"recorded": graphs.captures, "record_s": round(record_s, 2),
+                           "replays": graphs.replays, "eager_calls": graphs.eager_calls,
+                           "max_blocks_per_seq": graphs.width}),
     }
 
 
@@ -1319,8 +1459,10 @@ def main():
     line["decode_32k"]["traffic"] = traffic.get("decode_32k_bytes") if traffic else None
     line["accumulator"] = bench_accumulator(device)
     line["reference_shapes"] = bench_reference_shapes(device)
+    line["decode_runtime"] = bench_decode_runtime(device)
     if not args.no_serving:
         line["serving"] = bench_serving(device)
+        line["serving_decode_graphs"] = bench_serving(device, decode_graphs=True)
     print(json.dumps(line), flush=True)
 
 

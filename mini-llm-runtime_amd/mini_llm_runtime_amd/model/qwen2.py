@@ -267,8 +267,15 @@ class TinyQwen2Model(nn.Module):
             h, position_ids, kv_cache, i, slot_mapping, block_table, context_len))
 
     def forward_decode_batch_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
-                                        block_tables, context_lens) -> torch.Tensor:
-        """[B, 1] token ids -> [B, 1, hidden_size]."""
+                                        block_tables, context_lens, *,
+                                        metadata_checked: bool = False) -> torch.Tensor:
+        """[B, 1] token ids -> [B, 1, hidden_size].
+
+        metadata_checked: the caller already ran the device-side metadata
+        checks on these position, slot, block-table and length tensors against
+        this cache (Qwen2Attention._check_decode_metadata), so no layer runs
+        them and the call makes no host sync; the HIP-graph decode
+        (runtime/decode_graphs.py) checks before it copies its inputs in."""
         if input_ids.ndim != 2 or input_ids.shape[1] != 1:
             raise ValueError("input_ids must have shape [B, 1] for decode")
         if input_ids.shape[0] == 0:
@@ -290,7 +297,7 @@ class TinyQwen2Model(nn.Module):
         # repeat the checks.
         return self._run(input_ids, lambda layer, i, h: layer.forward_decode_batch_with_cache(
             h, position_ids, kv_cache, i, slot_mapping, block_tables, context_lens,
-            metadata_checked=i > 0))
+            metadata_checked=metadata_checked or i > 0))
 
     def forward_prefill_packed_with_cache(self, input_ids: torch.Tensor,
                                           position_ids: torch.Tensor,
@@ -413,11 +420,13 @@ class TinyQwen2ForCausalLM(nn.Module):
             slot_mapping=slot_mapping, block_table=block_table, context_len=context_len))
 
     def forward_decode_batch_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
-                                        block_tables, context_lens) -> torch.Tensor:
+                                        block_tables, context_lens, *,
+                                        metadata_checked: bool = False) -> torch.Tensor:
         """[B, 1] -> [B, 1, vocab_size] logits."""
         return self.lm_head(self.model.forward_decode_batch_with_cache(
             input_ids=input_ids, position_ids=position_ids, kv_cache=kv_cache,
-            slot_mapping=slot_mapping, block_tables=block_tables, context_lens=context_lens))
+            slot_mapping=slot_mapping, block_tables=block_tables, context_lens=context_lens,
+            metadata_checked=metadata_checked))
 
     def forward_prefill_packed_with_cache(self, input_ids, position_ids, kv_cache,
                                           slot_mapping, block_tables, query_start_loc,

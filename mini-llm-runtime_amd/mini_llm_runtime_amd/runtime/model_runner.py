@@ -15,6 +15,10 @@ whatever the order of phases in the batch. The batch checks are the
 reference's, with its messages and order, evaluated with two host syncs
 instead of several per request.
 
+With ``decode_graphs`` (runtime/decode_graphs.py) the decodes of a step
+replay a HIP graph of the batched decode forward, recorded once per batch
+size, instead of issuing its kernels from the host.
+
 ``run_generation_step`` also checks the decode workspaces once per step: a
 split merge that gave up waiting (it only writes NaN) raises
 ``DecodeMergeError`` there instead of reaching the sampled tokens unnoticed.
@@ -270,9 +274,17 @@ def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list
     return qsl, num_tokens
 
 
-def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> torch.Tensor:
-    """[num_packed_tokens, vocab_size] logits in packed token order."""
+def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
+                        decode_graphs=None) -> torch.Tensor:
+    """[num_packed_tokens, vocab_size] logits in packed token order.
+
+    decode_graphs: a DecodeGraphs (runtime/decode_graphs.py) of this model and
+    cache; the batch's decodes then replay its recorded step instead of
+    running the decode forward eagerly."""
     qsl, num_tokens = _check_batch(model, batch, kv_cache)
+    if decode_graphs is not None and (decode_graphs.model is not model
+                                      or decode_graphs.kv_cache is not kv_cache):
+        raise ValueError("decode_graphs must belong to this model and KV cache")
     device = batch.input_token_ids.device
     logits = model.lm_head.weight.new_empty((num_tokens, model.lm_head.out_features))
     prefill = [i for i, ph in enumerate(batch.request_phases) if ph is RequestStatus.PREFILLING]
@@ -304,13 +316,15 @@ def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tor
     if decode:
         req = torch.tensor(decode, dtype=torch.long, device=device)
         rows = torch.tensor([qsl[i] for i in decode], dtype=torch.long, device=device)
-        out = model.forward_decode_batch_with_cache(
-            input_ids=batch.input_token_ids.index_select(0, rows).unsqueeze(1),
-            position_ids=batch.positions.index_select(0, rows).unsqueeze(1),
-            kv_cache=kv_cache,
-            slot_mapping=batch.slot_mapping.index_select(0, rows),
-            block_tables=batch.block_tables.index_select(0, req),
-            context_lens=batch.context_lens.index_select(0, req))
+        step = dict(input_ids=batch.input_token_ids.index_select(0, rows).unsqueeze(1),
+                    position_ids=batch.positions.index_select(0, rows).unsqueeze(1),
+                    slot_mapping=batch.slot_mapping.index_select(0, rows),
+                    block_tables=batch.block_tables.index_select(0, req),
+                    context_lens=batch.context_lens.index_select(0, req))
+        if decode_graphs is not None:
+            out = decode_graphs(**step)
+        else:
+            out = model.forward_decode_batch_with_cache(kv_cache=kv_cache, **step)
         logits.index_copy_(0, rows, out.squeeze(1))
     return logits
 
@@ -336,7 +350,8 @@ def greedy_sample(packed_logits: torch.Tensor, batch: ModelBatch) -> dict[str, i
 
 
 def run_generation_step(model, scheduler: Scheduler,
-                        eos_token_id: int | None = None) -> GenerationStepResult:
+                        eos_token_id: int | None = None,
+                        decode_graphs=None) -> GenerationStepResult:
     if not scheduler.waiting and not scheduler.running:
         raise ValueError("Cannot run generation step with no requests")
     scheduler_output = scheduler.schedule()
@@ -344,7 +359,8 @@ def run_generation_step(model, scheduler: Scheduler,
         raise RuntimeError("Scheduler made no progress while unfinished requests remain")
     batch = build_model_batch(scheduler_output, block_size=scheduler.kv_cache.block_size,
                               device=scheduler.kv_cache.device)
-    packed_logits = execute_model_batch(model=model, batch=batch, kv_cache=scheduler.kv_cache)
+    packed_logits = execute_model_batch(model=model, batch=batch, kv_cache=scheduler.kv_cache,
+                                        decode_graphs=decode_graphs)
     sampled = greedy_sample(packed_logits, batch)
     if batch.input_token_ids.device.type == "cuda":
         # Before any sampled token is committed to the scheduler.
@@ -360,10 +376,11 @@ def run_generation_step(model, scheduler: Scheduler,
 
 
 def run_greedy_generation(model, scheduler: Scheduler,
-                          eos_token_id: int | None = None) -> list[Request]:
+                          eos_token_id: int | None = None,
+                          decode_graphs=None) -> list[Request]:
     """Schedule-model-sample-update until every request has finished."""
     finished: list[Request] = []
     while scheduler.waiting or scheduler.running:
-        finished.extend(run_generation_step(model, scheduler,
-                                            eos_token_id=eos_token_id).finished_requests)
+        finished.extend(run_generation_step(model, scheduler, eos_token_id=eos_token_id,
+                                            decode_graphs=decode_graphs).finished_requests)
     return finished

@@ -301,3 +301,24 @@ def test_serving_schedule_block_tables_match_oracle_allocator():
     # The run exercised admission, exit and reuse.
     steps_with_prefill = sum(any(rid.startswith("arr") for rid in ids[:2]) for ids, _, _ in runs[0])
     assert steps_with_prefill > 50
+
+
+def test_decode_graphs_need_a_hip_cache(tiny_cpu):
+    """The HIP-graph decode refuses a cache that is not on a HIP device."""
+    from mini_llm_runtime_amd.runtime.decode_graphs import DecodeGraphs
+
+    model, cache = tiny_cpu
+    with pytest.raises(ValueError, match="needs the KV cache on a HIP device"):
+        DecodeGraphs(model, cache, max_blocks_per_seq=4)
+
+
+def test_execute_model_batch_refuses_foreign_decode_graphs(tiny_cpu):
+    """decode_graphs of another model or cache is refused before any launch."""
+
+    class Foreign:
+        model = None
+        kv_cache = None
+
+    model, cache = tiny_cpu
+    with pytest.raises(ValueError, match="decode_graphs must belong to this model"):
+        execute_model_batch(model, good_batch(), cache, decode_graphs=Foreign())
