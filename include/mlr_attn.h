@@ -121,8 +121,8 @@ size_t mlr_paged_decode_workspace_size(int64_t batch, int64_t num_q_heads,
  *   tokens_per_split: split-KV granularity in tokens (<= 0: library default)
  *   workspace    : >= mlr_paged_decode_workspace_size(...) bytes, 256-aligned,
  *                  all-zero before its first use (hipMemset once). It holds
- *                  the splits' partial results; the matrix-core kernel (bf16
- *                  and FP32) merges them in the same launch (the workgroup of a
+ *                  the splits' partial results; the matrix-core kernel (bf16,
+ *                  fp16 and FP32) merges them in the same launch (the workgroup of a
  *                  sequence's last split waits for the words of the others
  *                  to arrive, a zero word meaning "not yet"). Every call
  *                  returns each word it wrote to zero, so the workspace can be
@@ -378,6 +378,38 @@ int mlr_build_step_metadata(const int64_t *req_info, const int64_t *block_tables
                             int64_t num_tokens, int64_t block_size, int64_t *positions,
                             int64_t *slot_mapping, int64_t *query_start_loc,
                             int64_t *context_lens, void *stream);
+
+/*
+ * RMSNorm of `rows` rows of `hidden` elements, after a residual add when
+ * `residual` is given:
+ *   r   = x + residual, rounded to the dtype and written to residual_out
+ *         (which may be residual itself); r = x without a residual
+ *   out = weight * dtype(r / sqrt(mean(r^2) + eps))
+ * Statistics in FP32 for bf16 and fp16; every step rounded as the PyTorch
+ * module's separate operations round it (only the order of the row sum
+ * differs). dtype bf16, fp16 or FP32; weight [hidden] of the same dtype; row
+ * strides in elements. out may be x.
+ *
+ * Replaces Qwen2RMSNorm.forward (model/qwen2.py:88-123) and the residual add
+ * before the post-attention norm of Qwen2DecoderLayer (:794-940).
+ */
+int mlr_rms_norm(const void *x, int64_t x_stride, const void *residual, int64_t residual_stride,
+                 void *residual_out, int64_t residual_out_stride, const void *weight, void *out,
+                 int64_t out_stride, int64_t rows, int64_t hidden, double eps, int dtype,
+                 void *stream);
+
+/*
+ * out[r, j] = dtype(silu(gate_up[r, j])) * gate_up[r, intermediate + j] for
+ * j < intermediate: the gate and up projections side by side in one row, as
+ * one GEMM with the two weights stacked writes them. silu(g) = g / (1 +
+ * expf(-g)) in FP32, rounded to the dtype, then the product rounded to the
+ * dtype, as F.silu(gate) * up rounds them. dtype bf16, fp16 or FP32.
+ *
+ * Replaces the activation and product of Qwen2MLP.forward
+ * (model/qwen2.py:768-792).
+ */
+int mlr_silu_mul(const void *gate_up, int64_t gate_up_stride, void *out, int64_t out_stride,
+                 int64_t rows, int64_t intermediate, int dtype, void *stream);
 
 /*
  * Diagnostics. No counterpart in the reference: a read-only pass that

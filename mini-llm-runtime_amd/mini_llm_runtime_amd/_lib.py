@@ -100,6 +100,13 @@ _PROTOTYPES = {
         [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,
          _c_ptr, _c_ptr, _c_ptr],
     ),
+    "mlr_rms_norm": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64,
+         _c_i64, _c_f64, _c_int, _c_ptr],
+    ),
+    "mlr_silu_mul": (
+        _c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr]),
     "mlr_paged_kv_read_floor_outputs": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "mlr_paged_kv_read_floor": (
         _c_int,

@@ -8,6 +8,11 @@ layers of ``Qwen2DecoderLayer``, norm) + lm_head (tied to the embedding when
 the config says so). Each layer is pre-norm attention + pre-norm SwiGLU MLP
 with residuals; RMSNorm keeps FP32 statistics for half-precision inputs.
 
+On a HIP device each RMSNorm, the residual add before the post-attention
+norm together with that norm, and the MLP's silu(gate) * up are one launch
+each (kernels/layer_ops.py), with the gate and up projections as one GEMM;
+the roundings are those of the PyTorch operations they replace.
+
 The attention is ``Qwen2Attention`` on the HIP kernels. Besides the
 reference's entry points, the model has ``forward_prefill_packed_with_cache``:
 the prompts (or prompt chunks) of several requests in one packed forward,
@@ -23,6 +28,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ..kernels import layer_ops as kops
 from ..runtime.paged_kv_cache import PagedKVCache
 from .qwen2_attention import Qwen2Attention, _raise_first
 
@@ -88,11 +94,32 @@ class Qwen2RMSNorm(nn.Module):
             raise ValueError("hidden_states last dimension must match hidden_size "
                              f"({self.weight.shape[0]}), got {hidden_states.shape[-1]}")
         dtype = hidden_states.dtype
+        if kops.supported(hidden_states):
+            # One launch (mlr_rms_norm), the same roundings as below.
+            return kops.rms_norm(hidden_states, self.weight.to(dtype), self.variance_epsilon)
         stats = torch.float32 if dtype in (torch.float16, torch.bfloat16) else dtype
         x = hidden_states.to(stats)
         normalized = x * torch.rsqrt(x.square().mean(dim=-1, keepdim=True)
                                      + self.variance_epsilon)
         return self.weight.to(dtype) * normalized.to(dtype)
+
+    def forward_with_residual(self, hidden_states: torch.Tensor,
+                              residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """(self(residual + hidden_states), residual + hidden_states): the
+        decoder layer's residual add and the norm after it, in one launch on a
+        HIP device."""
+        if hidden_states.shape != residual.shape:
+            raise ValueError("hidden_states and residual must have the same shape")
+        if hidden_states.shape[-1] != self.weight.shape[0]:
+            raise ValueError("hidden_states last dimension must match hidden_size "
+                             f"({self.weight.shape[0]}), got {hidden_states.shape[-1]}")
+        dtype = hidden_states.dtype
+        if (kops.supported(hidden_states) and residual.dtype == dtype
+                and residual.device == hidden_states.device):
+            return kops.rms_norm(hidden_states, self.weight.to(dtype), self.variance_epsilon,
+                                 residual=residual)
+        total = residual + hidden_states
+        return self(total), total
 
 
 class Qwen2MLP(nn.Module):
@@ -103,8 +130,26 @@ class Qwen2MLP(nn.Module):
         self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+        self._gate_up = None
+        self._gate_up_key = None
+
+    def _gate_up_weight(self) -> torch.Tensor:
+        """[gate; up] weight, concatenated once and rebuilt when either
+        parameter is replaced or changed in place."""
+        parts = (self.gate_proj.weight, self.up_proj.weight)
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in parts)
+        if key != self._gate_up_key:
+            with torch.no_grad():
+                self._gate_up = torch.cat(parts, dim=0)
+            self._gate_up_key = key
+        return self._gate_up
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        if kops.supported(hidden_states):
+            # One GEMM for both projections, then one launch for
+            # silu(gate) * up (mlr_silu_mul, the same roundings as below).
+            gate_up = F.linear(hidden_states, self._gate_up_weight())
+            return self.down_proj(kops.silu_mul(gate_up))
         return self.down_proj(F.silu(self.gate_proj(hidden_states)) * self.up_proj(hidden_states))
 
 
@@ -120,8 +165,9 @@ class Qwen2DecoderLayer(nn.Module):
                                                      eps=config.rms_norm_eps)
 
     def _block(self, hidden_states: torch.Tensor, attend) -> torch.Tensor:
-        hidden_states = hidden_states + attend(self.input_layernorm(hidden_states))
-        return hidden_states + self.mlp(self.post_attention_layernorm(hidden_states))
+        normed, hidden_states = self.post_attention_layernorm.forward_with_residual(
+            attend(self.input_layernorm(hidden_states)), hidden_states)
+        return hidden_states + self.mlp(normed)
 
     def forward(self, hidden_states: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
         return self._block(hidden_states, lambda h: self.self_attn(h, position_ids))
