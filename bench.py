@@ -33,13 +33,23 @@ decode); the read floor of the decode step (config.read_floor: a read-only
 pass over the same K/V rows through the same block tables,
 mlr_paged_kv_read_floor); the 8 x 32K decode over rotated pools, with its
 own read floor; the fused pre-attention step; the KV
-write on its own (``kv_write``); the FP32 batch-4 decode step; and
-``serving``, end-to-end continuous-batching steps of a random-init
-Qwen2.5-0.5B-shape model in BF16 (workloads.qwen05b_serving: about 48
-decodes + 2 x 1024-token prefills per step, 128 steps after the warm-up).
-``provenance`` names the sources and library the numbers come from.
+write on its own (``kv_write``); the FP32 batch-4 decode step;
+``reference_shapes``, the reference's own decode-kernel benchmark shape (one
+request, 32 q / 8 KV heads, head_dim 128, 512 to 16384 tokens, bf16 and fp16)
+beside its published latencies; ``decode_runtime``, the reference's own
+full-model batched decode-step cases (Qwen2.5-0.5B shape, B=8 at contexts
+288..512 and B=16 at 128, BF16 and FP32), eager and replayed from a HIP graph,
+beside its published step times; and ``serving`` / ``serving_decode_graphs``,
+end-to-end continuous-batching steps of a random-init Qwen2.5-0.5B-shape model
+in BF16 (workloads.qwen05b_serving: about 48 decodes + 2 x 1024-token
+prefills per step, 128 steps after the warm-up), eager and with the decode
+forward replayed from HIP graphs. ``provenance`` names the sources and
+library the numbers come from.
 
     python bench.py [--gpus 1] [--steps 240] [--warmup 48]
+
+``--serving`` runs only the serving steps (eager; with ``--decode-graphs``,
+the decode forward replayed from HIP graphs) and prints their line.
 
 ``--profile`` launches the same kernels eagerly and untimed, for rocprofv3:
 ``--steps`` decode steps over the rotated layers, one decode without the
@@ -89,6 +99,8 @@ def parse_args():
                    help="launch the kernels eagerly, untimed (for rocprofv3)")
     p.add_argument("--serving", action="store_true",
                    help="time only the end-to-end serving steps (qwen05b_serving, BF16)")
+    p.add_argument("--decode-graphs", action="store_true",
+                   help="with --serving: replay each step's decode forward from HIP graphs")
     p.add_argument("--no-serving", action="store_true",
                    help="leave the serving steps out of the default run")
     p.add_argument("--no-contiguous", action="store_true",
@@ -1365,7 +1377,8 @@ def main():
         return
     if args.serving:
         print(json.dumps({"metric": "serving step (qwen05b_serving, bf16)",
-                          **bench_serving(device)}), flush=True)
+                          **bench_serving(device, decode_graphs=args.decode_graphs)}),
+              flush=True)
         return
     dec = bench_decode(args, device)
     pre = None if args.no_prefill else bench_prefill(device)
