@@ -61,10 +61,11 @@ __device__ __forceinline__ SeqRange seq_range(const PrefillParams &p, int s) {
   return r;
 }
 
-// True when the bf16 matrix-core kernel covers these arguments (bf16, head_dim
-// 64 or 128, power-of-two block_size >= 16, aligned rows, positive scale).
+// True when the matrix-core kernel covers these arguments (bf16 or fp16,
+// head_dim 64 or 128, power-of-two block_size >= 16, aligned rows, positive
+// scale).
 bool prefill_mfma_eligible(const PrefillParams &p, int dtype);
-int launch_prefill_mfma(const PrefillParams &p, int64_t max_query_len,
+int launch_prefill_mfma(const PrefillParams &p, int dtype, int64_t max_query_len,
                         hipStream_t stream);
 
 }  // namespace mlr

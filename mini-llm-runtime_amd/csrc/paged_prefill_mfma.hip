@@ -1,4 +1,5 @@
-// bf16 paged chunk prefill on gfx950 matrix cores (v_mfma_f32_32x32x16_bf16).
+// bf16 and fp16 paged chunk prefill on gfx950 matrix cores
+// (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x16_f16).
 //
 // One workgroup = 128 queries of one query head and eight waves: two splits
 // of the key range (waves 0-3 and 4-7, merged through LDS at the end), each
@@ -33,7 +34,7 @@
 //   moves only when a tile raises the row max by more than kLazy, so
 //   probabilities stay below 2^kLazy and numerator and denominator share it.
 //   O^T[32 dims x 32 queries] += V^T[32 dims x 16 keys] . P^T[16 keys x 32 q]
-//       B = P^T packed to bf16 straight from the S^T registers (k slot
+//       B = P^T packed to the 16-bit type straight from the S^T registers (k slot
 //       8(l/32)+e <-> key 16kb + 8(e/4) + 4(l/32) + e%4), A = V^T from two
 //       ds_read_b64_tr_b16 per MFMA.
 //   The row sums add the FP32 probabilities, as the reference does.
@@ -47,7 +48,9 @@
 // differ from the reference and stay far inside the 2e-2 tolerance of its
 // bf16 tests: q*scale*log2(e) is rounded to bf16 (relative 2^-9 per element,
 // the size of the reference's own bf16 rounding of q.k at :411-413, which is
-// not done here), and P is rounded to bf16 as the MFMA operand.
+// not done here), and P is rounded to bf16 as the MFMA operand. fp16 runs the
+// same kernel with fp16 operands (the same two roundings, to fp16: relative
+// 2^-12), round-to-nearest-even throughout.
 #include "paged_prefill.h"
 
 #include <atomic>
@@ -57,6 +60,8 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -94,6 +99,34 @@ __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// The 16-bit operand type of the MFMAs: bf16 or fp16 fragments, the 32x32x16
+// MFMA of that type, two floats packed to it (round to nearest even), and the
+// two halves of a 32-bit word of it widened to FP32.
+template <typename T> struct Mma;
+template <> struct Mma<bf16_t> {
+  using v8 = bf16x8_t;
+  __device__ static f32x16_t mfma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack2(float lo, float hi) { return bf16_pack2(lo, hi); }
+  __device__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static uint32_t bits(float x) { return float_to_bf16_bits(x); }
+};
+template <> struct Mma<f16_t> {
+  using v8 = f16x8_t;
+  __device__ static f32x16_t mfma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack2(float lo, float hi) {
+    const f16x2_t v = __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t);
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static float lo(uint32_t w) { return f16_bits_to_float(static_cast<uint16_t>(w)); }
+  __device__ static float hi(uint32_t w) { return f16_bits_to_float(static_cast<uint16_t>(w >> 16)); }
+  __device__ static uint32_t bits(float x) { return float_to_f16_bits(x); }
+};
+
 // max(a, b, c) as one v_maximum3_f32 (NaN-propagating, no canonicalisation).
 __device__ __forceinline__ float max3(float a, float b, float c) {
   return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
@@ -128,10 +161,12 @@ __device__ __forceinline__ int workgroup_rank(int b, int nwg, int ncu, int pair_
   return b < paired ? single + b : b - paired;
 }
 
-template <int D, int BN, int KS>
+template <typename T, int D, int BN, int KS>
 __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2)))
 void prefill_mfma(PrefillParams p) {
   using C = Cfg<D, BN>;
+  using M = Mma<T>;
+  using v8 = typename M::v8;
   constexpr int QS = D / 16;         // 16-dim k-steps of S^T
   constexpr int NB = D / 32;         // 32-dim blocks of O^T
   constexpr int KB = C::kBlocks;     // 32-key blocks per tile
@@ -247,7 +282,7 @@ void prefill_mfma(PrefillParams p) {
   uint4 qraw[QS];
 #pragma unroll
   for (int s = 0; s < QS; ++s) qraw[s] = *reinterpret_cast<const uint4 *>(qrow + 16 * s + 8 * hh);
-  bf16x8_t qf[QS];
+  v8 qf[QS];
 
   // Copy role: copy i of a span moves chunk positions [64i, 64i + 64) of its 16
   // rows; lane l fills position 64i + l (row rr, physical chunk pc) with
@@ -326,9 +361,8 @@ void prefill_mfma(PrefillParams p) {
     for (int j = 0; j < KB; ++j) {
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
-        const bf16x8_t a =
-            *reinterpret_cast<const bf16x8_t *>(kst + 32 * j * C::kRowB + koff[st]);
-        s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[st], st == 0 ? negm : s[j], 0, 0, 0);
+        const v8 a = *reinterpret_cast<const v8 *>(kst + 32 * j * C::kRowB + koff[st]);
+        s[j] = M::mfma(a, qf[st], st == 0 ? negm : s[j]);
       }
     }
     // At most two K reads ahead of the MFMAs (four VGPRs each): hoisting all
@@ -458,7 +492,7 @@ void prefill_mfma(PrefillParams p) {
     }
     if (bad != nullptr) bad[4 * lane + w] = static_cast<unsigned char>(sp.bad);
   };
-  // exp2 of a tile's S^T packed to bf16 (the P@V operand), with the FP32
+  // exp2 of a tile's S^T packed to the 16-bit type (the P@V operand), with the FP32
   // probabilities added to the row sum (four chains).
   auto probs = [&](const f32x16_t (&sc)[KB], uint32_t (&pk)[KB][8]) __attribute__((always_inline)) {
     float lsum[4];
@@ -468,7 +502,7 @@ void prefill_mfma(PrefillParams p) {
       for (int x = 0; x < 8; ++x) {
         const float p0 = __builtin_amdgcn_exp2f(sc[j][2 * x]);
         const float p1 = __builtin_amdgcn_exp2f(sc[j][2 * x + 1]);
-        pk[j][x] = bf16_pack2(p0, p1);
+        pk[j][x] = M::pack2(p0, p1);
         if (j == 0 && x < 2) {
           lsum[2 * x] = p0;
           lsum[2 * x + 1] = p1;
@@ -488,9 +522,9 @@ void prefill_mfma(PrefillParams p) {
 #pragma unroll
       for (int h16 = 0; h16 < 2; ++h16) {
         const int kb = 2 * j + h16;  // 16-key block
-        const bf16x8_t pb = __builtin_bit_cast(
-            bf16x8_t, make_uint4(pk[j][4 * h16], pk[j][4 * h16 + 1], pk[j][4 * h16 + 2],
-                                 pk[j][4 * h16 + 3]));
+        const v8 pb = __builtin_bit_cast(
+            v8, make_uint4(pk[j][4 * h16], pk[j][4 * h16 + 1], pk[j][4 * h16 + 2],
+                           pk[j][4 * h16 + 3]));
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
           const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -498,8 +532,8 @@ void prefill_mfma(PrefillParams p) {
           const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_s16x4_t *)(vst + 16 * kb * C::kRowB + voff[1][n]));
           const uint2 ulo = __builtin_bit_cast(uint2, lo), uhi = __builtin_bit_cast(uint2, hi);
-          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(ulo.x, ulo.y, uhi.x, uhi.y));
-          acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, acc[n], 0, 0, 0);
+          const v8 a = __builtin_bit_cast(v8, make_uint4(ulo.x, ulo.y, uhi.x, uhi.y));
+          acc[n] = M::mfma(a, pb, acc[n]);
         }
       }
     // Two MFMAs' V^T reads (two each) ahead of the MFMAs.
@@ -518,7 +552,7 @@ void prefill_mfma(PrefillParams p) {
   // softmax phase V_i, with a workgroup barrier after each phase:
   //   M_i: O^T += V^T P^T of tile i - 1, S^T of tile i, and the scalar
   //        set-up of the copies V_i will issue;
-  //   V_i: issue those copies, then mask, row max, rescale, exp2 and bf16
+  //   V_i: issue those copies, then mask, row max, rescale, exp2 and 16-bit
   //        packing of tile i, with the FP32 row sums.
   // Split 1 passes one extra barrier first, so it runs a phase behind split
   // 0 and on every SIMD one wave's matrix-core work overlaps the other's
@@ -559,9 +593,8 @@ void prefill_mfma(PrefillParams p) {
     uint32_t o4[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      o4[e] = bf16_pack2(__uint_as_float(w4[e] << 16) * c2,
-                         __uint_as_float(w4[e] & 0xffff0000u) * c2);
-    qf[s] = __builtin_bit_cast(bf16x8_t, make_uint4(o4[0], o4[1], o4[2], o4[3]));
+      o4[e] = M::pack2(M::lo(w4[e]) * c2, M::hi(w4[e]) * c2);
+    qf[s] = __builtin_bit_cast(v8, make_uint4(o4[0], o4[1], o4[2], o4[3]));
   }
   if (split == 1) __builtin_amdgcn_s_barrier();
   // S^T (M to V) and packed P (V to M) are defined in every phase, idle
@@ -686,16 +719,14 @@ void prefill_mfma(PrefillParams p) {
         // acc[n][4g4 + e] = O[query][32n + 8g4 + 4hh + e].
         const f32x16_t &a = acc[n];
         const uint2 v = make_uint2(
-            (uint32_t)float_to_bf16_bits(a[4 * g4] * inv) |
-                ((uint32_t)float_to_bf16_bits(a[4 * g4 + 1] * inv) << 16),
-            (uint32_t)float_to_bf16_bits(a[4 * g4 + 2] * inv) |
-                ((uint32_t)float_to_bf16_bits(a[4 * g4 + 3] * inv) << 16));
+            M::bits(a[4 * g4] * inv) | (M::bits(a[4 * g4 + 1] * inv) << 16),
+            M::bits(a[4 * g4 + 2] * inv) | (M::bits(a[4 * g4 + 3] * inv) << 16));
         *reinterpret_cast<uint2 *>(orow + 32 * n + 8 * g4 + 4 * hh_e) = v;
       }
   }
 }
 
-template <int D, int BN, int KS>
+template <typename T, int D, int BN, int KS>
 int launch(const PrefillParams &p, int64_t max_query_len, hipStream_t stream) {
   PrefillParams q = p;
   q.n_qtiles = static_cast<int>(ceil_div(max_query_len, kBM));
@@ -713,7 +744,7 @@ int launch(const PrefillParams &p, int64_t max_query_len, hipStream_t stream) {
     int ncu = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void *>(prefill_mfma<D, BN, KS>), 256 * KS, 0) !=
+            &per_cu, reinterpret_cast<const void *>(prefill_mfma<T, D, BN, KS>), 256 * KS, 0) !=
             hipSuccess)
       return set_error(MLR_ERR_HIP, "mlr_paged_prefill: device query failed");
     per_cu_of[dev].store(per_cu, std::memory_order_relaxed);
@@ -721,7 +752,7 @@ int launch(const PrefillParams &p, int64_t max_query_len, hipStream_t stream) {
   }
   q.ncu = ncu_of[dev].load(std::memory_order_acquire);
   q.pair_cu = per_cu_of[dev].load(std::memory_order_relaxed) == 2 ? 1 : 0;
-  prefill_mfma<D, BN, KS><<<dim3(static_cast<unsigned>(blocks)), 256 * KS, 0, stream>>>(q);
+  prefill_mfma<T, D, BN, KS><<<dim3(static_cast<unsigned>(blocks)), 256 * KS, 0, stream>>>(q);
   return check_launch("mlr_paged_prefill(mfma)");
 }
 
@@ -737,17 +768,22 @@ bool prefill_mfma_eligible(const PrefillParams &p, int dtype) {
   // Positions, block ids and in-block byte offsets are 32-bit inside the
   // kernel; a 16-row span must fit a block.
   constexpr int64_t k2g = int64_t(1) << 31;
-  return dtype == MLR_DTYPE_BF16 && (p.d == 64 || p.d == 128) && aligned &&
+  return (dtype == MLR_DTYPE_BF16 || dtype == MLR_DTYPE_F16) && (p.d == 64 || p.d == 128) &&
+         aligned &&
          p.bs_log2 >= 4 && p.max_blocks * p.block_size < k2g && p.num_blocks < k2g &&
          p.block_size * p.hkv * p.d * 2 < k2g && p.scale > 0.0 && p.scale < 1e30;
 }
 
-int launch_prefill_mfma(const PrefillParams &p, int64_t max_query_len,
+int launch_prefill_mfma(const PrefillParams &p, int dtype, int64_t max_query_len,
                         hipStream_t stream) {
   // The reference's tile_size only orders the FP32 accumulation; the kernel's
   // key tile is fixed per head_dim by its LDS budget.
-  if (p.d == 64) return launch<64, 64, 2>(p, max_query_len, stream);
-  return launch<128, 64, 2>(p, max_query_len, stream);
+  if (dtype == MLR_DTYPE_F16) {
+    if (p.d == 64) return launch<f16_t, 64, 64, 2>(p, max_query_len, stream);
+    return launch<f16_t, 128, 64, 2>(p, max_query_len, stream);
+  }
+  if (p.d == 64) return launch<bf16_t, 64, 64, 2>(p, max_query_len, stream);
+  return launch<bf16_t, 128, 64, 2>(p, max_query_len, stream);
 }
 
 }  // namespace mlr

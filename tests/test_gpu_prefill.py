@@ -59,7 +59,10 @@ CASES = [
     (torch.bfloat16, 14, 2, 64, 16, 1000, 77, 128),
     (torch.bfloat16, 28, 4, 128, 16, 300, 200, 16),
     (torch.bfloat16, 8, 8, 64, 32, 17, 100, 64),
-    (torch.float16, 14, 2, 64, 16, 100, 130, 64),
+    (torch.float16, 14, 2, 64, 16, 100, 130, 64),                  # fp16 matrix cores
+    (torch.float16, 28, 4, 128, 16, 300, 200, 16),                 # fp16, D=128
+    (torch.float16, 8, 8, 64, 32, 17, 100, 64),                    # fp16, G=1, BS=32
+    (torch.float16, 14, 2, 64, 16, 1000, 77, 128),
     (torch.float32, 14, 2, 64, 16, 250, 70, 64),
     (torch.float32, 6, 3, 40, 5, 11, 29, 7),
     (torch.float64, 4, 2, 16, 4, 9, 13, 4),
@@ -145,6 +148,20 @@ EDGE_CASES = [
                               for c in EDGE_CASES])
 def test_bf16_tiling_edges_match_oracle(device, hq, hkv, d, bs, prefix, chunk):
     q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, torch.bfloat16,
+                                 seed=prefix + chunk)
+    want = opa.prefill_chunk_tiled(q, kc, vc, table, prefix, prefix + chunk, bs, 64)
+    got = kpa.paged_attention_prefill_chunk_tiled(
+        q.to(device), kc.to(device), vc.to(device), table, prefix, prefix + chunk, bs, 64)
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) <= 2e-2
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs,prefix,chunk", EDGE_CASES,
+                         ids=[f"{c[0]}x{c[1]}-d{c[2]}-bs{c[3]}-p{c[4]}-c{c[5]}"
+                              for c in EDGE_CASES])
+def test_fp16_tiling_edges_match_oracle(device, hq, hkv, d, bs, prefix, chunk):
+    """The same tiling edges in fp16 (the matrix-core kernel's fp16 operands)."""
+    q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, torch.float16,
                                  seed=prefix + chunk)
     want = opa.prefill_chunk_tiled(q, kc, vc, table, prefix, prefix + chunk, bs, 64)
     got = kpa.paged_attention_prefill_chunk_tiled(

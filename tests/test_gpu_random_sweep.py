@@ -21,7 +21,8 @@ the exact result can differ by more than 2e-2 (measured on the CPU for one
 such case: oracle 0.019 from float64 attention, an emulation of the kernel's
 roundings 0.0085). So each element is checked against float64 attention
 within 2e-2 plus half a bf16 ulp of its value (2^-8 |x|), and against the
-oracle within 2e-2 plus one ulp (2^-7 |x|).
+oracle within 2e-2 plus one ulp (2^-7 |x|). The fp16 sweep draws the same
+kinds of shapes in fp16, with fp16's half ulp and ulp (2^-11, 2^-10).
 """
 
 from __future__ import annotations
@@ -132,7 +133,23 @@ def prefill_case(seed):
 
 @pytest.mark.parametrize("seed", range(32))
 def test_random_varlen_prefill_matches_oracle(device, seed):
-    c = prefill_case(seed)
+    _check_random_prefill(device, seed, prefill_case(seed))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_varlen_prefill_fp16_matches_oracle(device, seed):
+    """The same draws in fp16: the matrix-core kernel with fp16 operands, or
+    the generic kernel where the shape sends it there."""
+    c = prefill_case(100 + seed)
+    c["dtype"] = torch.float16
+    _check_random_prefill(device, seed, c)
+
+
+# Half a unit and one unit in the last place of each 16-bit type, relative.
+HALF_ULP = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+
+
+def _check_random_prefill(device, seed, c):
     dtype, d, hq, hkv, bs = (c[k] for k in ("dtype", "d", "hq", "hkv", "bs"))
     qlens, prefixes, tile = c["qlens"], c["prefixes"], c["tile"]
     what = (f"seed {seed}: {str(dtype)[6:]} d{d} {hq}x{hkv} bs{bs} tile{tile} "
@@ -176,8 +193,9 @@ def test_random_varlen_prefill_matches_oracle(device, seed):
             continue
         exact = exact_prefill(q[lo:hi], *rows[s], prefixes[s])
         want = want.double()
-        err_exact = ((mine - exact).abs() - (2e-2 + 2.0 ** -8 * exact.abs())).max().item()
-        err_oracle = ((mine - want).abs() - (2e-2 + 2.0 ** -7 * want.abs())).max().item()
+        half = HALF_ULP[dtype]
+        err_exact = ((mine - exact).abs() - (2e-2 + half * exact.abs())).max().item()
+        err_oracle = ((mine - want).abs() - (2e-2 + 2 * half * want.abs())).max().item()
         assert err_exact <= 0, f"{what}: sequence {s} exceeds the bar against float64 " \
                                f"by {err_exact:.3g}"
         assert err_oracle <= 0, f"{what}: sequence {s} exceeds the bar against the oracle " \
