@@ -185,15 +185,15 @@ int mlr_paged_decode_append(
  * (:614-621; kernels/reference/paged_attention.py:178-254). Results equal
  * mlr_qkv_rope_write (positions = context_lens - 1, no bias) followed by
  * mlr_paged_decode bit for bit: the rotation rounds like the reference, each
- * bf16 product and sum rounded once, cos and sin of the position rounded to
- * bf16.
+ * bf16 (fp16) product and sum rounded once, cos and sin of the position
+ * rounded to bf16 (fp16).
  *   qkv      : [batch, (num_q_heads + 2 num_kv_heads) * head_dim], row stride
  *              qkv_stride_b, heads in the order q, k, v: the output of the
  *              projection (Qwen2QKVProjection, :211-236) with its bias,
  *              16-byte aligned rows
  *   inv_freq : FP32 [head_dim / 2], the rotary module's inverse frequencies
  *   slot_mapping : int64 [batch], the slot of position context_lens[b] - 1
- * Other arguments as for mlr_paged_decode. bf16 with head_dim 64 or 128, at
+ * Other arguments as for mlr_paged_decode. bf16 or fp16 with head_dim 64 or 128, at
  * most 16 query heads per KV head and block_size a multiple of 16 only (other
  * shapes: MLR_ERR_INVALID; run mlr_qkv_rope_write, then mlr_paged_decode).
  * No counterpart of its own in the reference: it fuses the calls above.

@@ -463,8 +463,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                               app->sb % 8 == 0 && app->sh % 8 == 0;
     if (app->inv_freq != nullptr) {
       // The fused rotary embedding exists on the matrix-core kernel only.
-      MLR_REQUIRE(mfma && dtype == MLR_DTYPE_BF16 && rows_aligned,
-                  "mlr_paged_decode_qkv: needs bf16, head_dim 64 or 128, at most 16 query "
+      MLR_REQUIRE(mfma && (dtype == MLR_DTYPE_BF16 || dtype == MLR_DTYPE_F16) && rows_aligned,
+                  "mlr_paged_decode_qkv: needs bf16 or fp16, head_dim 64 or 128, at most 16 query "
                   "heads per KV head, block_size a multiple of 16 and 16-byte aligned rows");
       p.inv_freq = app->inv_freq;
     }

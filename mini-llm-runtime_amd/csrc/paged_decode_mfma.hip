@@ -124,6 +124,11 @@ __device__ __forceinline__ float bf16_elem(const uint4 &v, int e) {
   return bf16_bits_to_float((e & 1) ? (w >> 16) : (w & 0xffffu));
 }
 
+__device__ __forceinline__ float f16_elem(const uint4 &v, int e) {
+  const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
+  return f16_bits_to_float(static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
 // a and b rounded to fp16 (nearest even) and back to FP32.
 __device__ __forceinline__ void f16_round2(float &a, float &b) {
   typedef float f32x2_v __attribute__((ext_vector_type(2)));
@@ -149,6 +154,7 @@ template <> struct Half16<bf16_t> {
   using v8 = bf16x8_t;
   __device__ static void round2(float &a, float &b) { bf16_round2(a, b); }
   __device__ static uint32_t pack2(float lo, float hi) { return bf16_pack2(lo, hi); }
+  __device__ static float elem(const uint4 &v, int e) { return bf16_elem(v, e); }
   __device__ static f32x4_t qk(uint4 k, v8 q, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, k), q, c, 0, 0, 0);
   }
@@ -161,6 +167,7 @@ template <> struct Half16<f16_t> {
   using v8 = f16x8_t;
   __device__ static void round2(float &a, float &b) { f16_round2(a, b); }
   __device__ static uint32_t pack2(float lo, float hi) { return f16_pack2(lo, hi); }
+  __device__ static float elem(const uint4 &v, int e) { return f16_elem(v, e); }
   __device__ static f32x4_t qk(uint4 k, v8 q, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, k), q, c, 0, 0, 0);
   }
@@ -171,19 +178,23 @@ template <> struct Half16<f16_t> {
   __device__ static uint16_t store(float x) { return float_to_f16_bits(x); }
 };
 
-// Rotary embedding of one (x[i], x[i + d/2]) pair in bf16 as the reference's
-// apply_rotary_pos_emb computes it (model/qwen2.py:125-209), operation by
-// operation: each product and the sum rounded to bf16 (nearest even), no
-// fused multiply-add. The products are rounded here, two at a time through
-// v_cvt_pk_bf16_f32; the sums come back unrounded, and bf16_pack2 rounds
-// them as it packs two outputs into one word.
+// Rotary embedding of one (x[i], x[i + d/2]) pair in bf16 or fp16 as the
+// reference's apply_rotary_pos_emb computes it (model/qwen2.py:125-209),
+// operation by operation: each product and the sum rounded to the 16-bit type
+// (nearest even), no fused multiply-add. The products are rounded here, two
+// at a time (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32); the sums come back
+// unrounded, and Half16<T>::pack2 rounds them as it packs two outputs into one
+// word. (For fp16, rounding an FP32 sum or product of two fp16 values to fp16
+// equals rounding the exact result once: FP32 carries more than 2 x 11 + 2
+// bits.)
+template <typename T>
 __device__ __forceinline__ void rope_pair(float x_lo, float x_hi, float c, float s,
                                           float &sum_lo, float &sum_hi) {
 #pragma clang fp contract(off)
   float a = x_lo * c, b = -x_hi * s;
   float e = x_hi * c, f = x_lo * s;
-  bf16_round2(a, b);
-  bf16_round2(e, f);
+  Half16<T>::round2(a, b);
+  Half16<T>::round2(e, f);
   sum_lo = a + b;
   sum_hi = e + f;
 }
@@ -644,7 +655,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
   static_assert(kF32 || kBf16 || std::is_same<T, f16_t>::value, "bf16, fp16 or FP32 elements");
   static_assert(!kF32 || !kLds, "the LDS tile is for 16-bit elements");
-  static_assert(!kRope || kBf16, "the rotary embedding is bf16");
+  static_assert(!kRope || !kF32, "the rotary embedding is bf16 or fp16");
   using S = typename TileTraits<T, D>::S;  // storage element
   constexpr int QK = TileTraits<T, D>::kKChunks;
   constexpr int kSize = static_cast<int>(sizeof(T));
@@ -724,7 +735,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         (int64_t)kvh * p.new_sh + new_off);
   // Fused rotary embedding (p.inv_freq set; fused write only): every wave
   // puts cos and sin of the decode position ctx - 1 for the d/2 frequencies,
-  // rounded to bf16, in its own LDS row and rotates q and the new K row with
+  // rounded to the 16-bit type, in its own LDS row and rotates q and the new K row with
   // them, as the fused pre-attention kernel does (qkv_rope.hip), once the
   // tile loads are in flight. The frequency is loaded here, before the tile
   // loads: memory loads complete in order, so a load issued after them
@@ -752,13 +763,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   // (no instruction) keeps the compiler from moving the other lanes' reads
   // above those writes.
   auto rotate_q = [&]() {
-    if constexpr (kBf16) {
+    if constexpr (kRope) {
+    using H = Half16<T>;
     if (lane < D / 2) {
       // sincosf shares one argument reduction between the two; its results
       // are those of cosf and sinf.
       float sn, cs;
       sincosf(static_cast<float>(ctx - 1) * rope_freq, &sn, &cs);
-      bf16_round2(cs, sn);
+      H::round2(cs, sn);
       rope_s[wave][lane] = cs;
       rope_s[wave][D / 2 + lane] = sn;
     }
@@ -770,13 +782,13 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
       float lo[8], hi[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        rope_pair(bf16_elem(qraw[j], e), bf16_elem(qraw[j + QK / 2], e), rope_s[wave][i0 + e],
-                  rope_s[wave][D / 2 + i0 + e], lo[e], hi[e]);
-      qf[j] = __builtin_bit_cast(bf16x8_t, make_uint4(bf16_pack2(lo[0], lo[1]), bf16_pack2(lo[2], lo[3]),
-                                                      bf16_pack2(lo[4], lo[5]), bf16_pack2(lo[6], lo[7])));
+        rope_pair<T>(H::elem(qraw[j], e), H::elem(qraw[j + QK / 2], e), rope_s[wave][i0 + e],
+                     rope_s[wave][D / 2 + i0 + e], lo[e], hi[e]);
+      qf[j] = __builtin_bit_cast(QF, make_uint4(H::pack2(lo[0], lo[1]), H::pack2(lo[2], lo[3]),
+                                                H::pack2(lo[4], lo[5]), H::pack2(lo[6], lo[7])));
       qf[j + QK / 2] =
-          __builtin_bit_cast(bf16x8_t, make_uint4(bf16_pack2(hi[0], hi[1]), bf16_pack2(hi[2], hi[3]),
-                                                  bf16_pack2(hi[4], hi[5]), bf16_pack2(hi[6], hi[7])));
+          __builtin_bit_cast(QF, make_uint4(H::pack2(hi[0], hi[1]), H::pack2(hi[2], hi[3]),
+                                            H::pack2(hi[4], hi[5]), H::pack2(hi[6], hi[7])));
     }
     }
   };
@@ -823,7 +835,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
   auto stage_new_row = [&]() {
     if (!new_owner) return;  // uniform
     uint4 v = new_chunk;
-    if (rope) {
+    if constexpr (kRope) {
+      using H = Half16<T>;
       uint4 xp;
       xp.x = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v.x), D / 16, 64));
       xp.y = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v.y), D / 16, 64));
@@ -835,14 +848,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkIte
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float x = bf16_elem(v, e), xo = bf16_elem(xp, e);
+          const float x = H::elem(v, e), xo = H::elem(xp, e);
           float ol, oh;
-          rope_pair(low ? x : xo, low ? xo : x, rope_s[wave][i0 + e],
-                    rope_s[wave][D / 2 + i0 + e], ol, oh);
+          rope_pair<T>(low ? x : xo, low ? xo : x, rope_s[wave][i0 + e],
+                       rope_s[wave][D / 2 + i0 + e], ol, oh);
           o[e] = low ? ol : oh;
         }
-        v = make_uint4(bf16_pack2(o[0], o[1]), bf16_pack2(o[2], o[3]), bf16_pack2(o[4], o[5]),
-                       bf16_pack2(o[6], o[7]));
+        v = make_uint4(H::pack2(o[0], o[1]), H::pack2(o[2], o[3]), H::pack2(o[4], o[5]),
+                       H::pack2(o[6], o[7]));
       }
     }
     if (lane < 2 * kRowChunks) {
@@ -1273,19 +1286,19 @@ int launch_one(const DecodeParams &p, hipStream_t stream) {
 
 // The three variants of one layout: decode only, with the fused KV write,
 // and with the fused write and rotary embedding (their own instantiations,
-// so the rotary code costs the other two nothing; bf16 only).
+// so the rotary code costs the other two nothing; bf16 and fp16).
 template <typename T, int D, int B, bool DB, bool L, int H = 1, int W = kWaves>
 int launch_variant(const DecodeParams &p, hipStream_t stream) {
   if (p.new_k == nullptr) return launch_one<T, D, B, DB, false, L, H, false, W>(p, stream);
-  if constexpr (std::is_same<T, bf16_t>::value) {
+  if constexpr (!std::is_same<T, float>::value) {
     if (p.inv_freq != nullptr) return launch_one<T, D, B, DB, true, L, H, true, W>(p, stream);
   }
   return launch_one<T, D, B, DB, true, L, H, false, W>(p, stream);
 }
 
 // bf16 and fp16 instantiations: head_dim x (one load batch | + LDS tile |
-// double-buffered) x KV heads per workgroup x variant (the rotary variant is
-// bf16 only).
+// double-buffered) x KV heads per workgroup x variant (with or without the
+// rotary embedding).
 template <typename T>
 int launch_16bit(const DecodeParams &p, int tiles_per_wave, bool pairs, hipStream_t stream) {
   if (p.d == 64) {

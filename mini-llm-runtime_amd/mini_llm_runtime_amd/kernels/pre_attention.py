@@ -116,11 +116,11 @@ def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, inv_freq: torch.T
 
 def qkv_rope_decode_fusable(qkv_dtype: torch.dtype, kv_cache: PagedKVCache,
                             num_q_heads: int) -> bool:
-    """Shapes ``qkv_rope_decode`` covers: bf16, head_dim 64 or 128, at most 16
-    query heads per KV head, block_size a multiple of 16, the cache in the
-    model dtype. Other shapes run qkv_rope_write and then the decode."""
+    """Shapes ``qkv_rope_decode`` covers: bf16 or fp16, head_dim 64 or 128, at
+    most 16 query heads per KV head, block_size a multiple of 16, the cache in
+    the model dtype. Other shapes run qkv_rope_write and then the decode."""
     hkv = kv_cache.num_kv_heads
-    return (qkv_dtype == torch.bfloat16 and kv_cache.dtype == torch.bfloat16
+    return (qkv_dtype in (torch.bfloat16, torch.float16) and kv_cache.dtype == qkv_dtype
             and kv_cache.head_dim in (64, 128) and num_q_heads % hkv == 0
             and 0 < num_q_heads // hkv <= 16 and kv_cache.block_size % 16 == 0)
 
@@ -147,7 +147,7 @@ def qkv_rope_decode(qkv: torch.Tensor, inv_freq: torch.Tensor, kv_cache: PagedKV
         raise IndexError("Unexpected layer_idx")
     hkv, d = kv_cache.num_kv_heads, kv_cache.head_dim
     if not qkv_rope_decode_fusable(qkv.dtype, kv_cache, num_q_heads):
-        raise ValueError("qkv_rope_decode needs bf16, head_dim 64 or 128, at most 16 query "
+        raise ValueError("qkv_rope_decode needs bf16 or fp16, head_dim 64 or 128, at most 16 query "
                          "heads per KV head and a block_size multiple of 16")
     width = (num_q_heads + 2 * hkv) * d
     if qkv.ndim != 2 or qkv.shape[1] != width or qkv.shape[0] == 0:

@@ -52,11 +52,11 @@ CASES = [
 ]
 
 
-def _case(hq, hkv, d, lens, seed):
-    _, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, BS, dtype=torch.bfloat16,
+def _case(hq, hkv, d, lens, seed, dtype=torch.bfloat16):
+    _, kc, vc, bt, sl, tables = random_paged(lens, hq, hkv, d, BS, dtype=dtype,
                                              seed=seed, fill=0.0)
     gen = torch.Generator().manual_seed(seed + 7)
-    qkv = torch.randn(len(lens), (hq + 2 * hkv) * d, generator=gen).bfloat16()
+    qkv = torch.randn(len(lens), (hq + 2 * hkv) * d, generator=gen).to(dtype)
     slots = torch.tensor([tables[b][(n - 1) // BS] * BS + (n - 1) % BS
                           for b, n in enumerate(lens)])
     return qkv, kc, vc, bt, sl, slots, tables
@@ -76,11 +76,13 @@ def _two_launches(qkv, inv_freq, cache, bt, sl, slots, hq, tokens_per_split):
     return kpa.paged_decode_launch(q, k, v, bt, sl, tokens_per_split=tokens_per_split), q
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("cid,hq,hkv,d,lens,tokens_per_split", CASES,
                          ids=[c[0] for c in CASES])
 def test_one_launch_equals_rope_write_then_decode(device, cid, hq, hkv, d, lens,
-                                                  tokens_per_split):
-    qkv, kc, vc, bt, sl, slots, tables = _case(hq, hkv, d, lens, seed=len(lens) * 31 + d + hq)
+                                                  tokens_per_split, dtype):
+    qkv, kc, vc, bt, sl, slots, tables = _case(hq, hkv, d, lens, seed=len(lens) * 31 + d + hq,
+                                               dtype=dtype)
     inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
     qkv, bt, sl, slots = (t.to(device) for t in (qkv, bt, sl, slots))
 
@@ -99,13 +101,15 @@ def test_one_launch_equals_rope_write_then_decode(device, cid, hq, hkv, d, lens,
     assert (got.double().cpu() - oracle.double()).abs().max().item() <= 2e-2
 
 
-def test_bf16_inv_freq_and_strided_qkv_rows(device):
-    """A model cast to bf16 holds inv_freq in bf16 (used as its FP32 value, as
-    qkv_rope_write does), and qkv rows may come from a wider buffer."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_half_inv_freq_and_strided_qkv_rows(device, dtype):
+    """A model cast to bf16 (fp16) holds inv_freq in bf16 (fp16), used as its
+    FP32 value as qkv_rope_write does, and qkv rows may come from a wider
+    buffer."""
     hq, hkv, d, lens = 14, 2, 64, [40, 1, 333]
-    qkv, kc, vc, bt, sl, slots, _ = _case(hq, hkv, d, lens, seed=3)
-    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device, torch.bfloat16)
-    wide = torch.zeros(len(lens), qkv.shape[1] + 64, dtype=torch.bfloat16)
+    qkv, kc, vc, bt, sl, slots, _ = _case(hq, hkv, d, lens, seed=3, dtype=dtype)
+    inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device, dtype)
+    wide = torch.zeros(len(lens), qkv.shape[1] + 64, dtype=dtype)
     wide[:, :qkv.shape[1]] = qkv
     wide, bt, sl, slots = (t.to(device) for t in (wide, bt, sl, slots))
     rows = wide[:, :qkv.shape[1]]
@@ -284,9 +288,20 @@ def test_random_served_steps_equal_the_two_launches(device, seed):
     """Seeded random shapes of the one-launch served step: equal to
     mlr_qkv_rope_write followed by the decode bit for bit (output and cache),
     and within 2e-2 of the oracle's decode."""
+    _check_random_served(device, seed, torch.bfloat16)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_served_steps_fp16(device, seed):
+    """The same in fp16 (other draws)."""
+    _check_random_served(device, 100 + seed, torch.float16)
+
+
+def _check_random_served(device, seed, dtype):
     d, hq, hkv, lens, ts = _random_served_case(seed)
-    shape = f"seed {seed}: d={d} hq={hq} hkv={hkv} batch={len(lens)} ts={ts} lens={lens}"
-    qkv, kc, vc, bt, sl, slots, tables = _case(hq, hkv, d, lens, seed=500 + seed)
+    shape = (f"seed {seed} {str(dtype)[6:]}: d={d} hq={hq} hkv={hkv} batch={len(lens)} "
+             f"ts={ts} lens={lens}")
+    qkv, kc, vc, bt, sl, slots, tables = _case(hq, hkv, d, lens, seed=500 + seed, dtype=dtype)
     inv_freq = Qwen2RotaryEmbedding(d, THETA).inv_freq.to(device)
     qkv, bt, sl, slots = (t.to(device) for t in (qkv, bt, sl, slots))
 
