@@ -527,12 +527,13 @@ def bench_decode(args, device):
     }
 
 
-def bench_prefill(device, reps=5, calls_per_graph=10):
+def bench_prefill(device, reps=5, calls_per_graph=10, dtype=None):
     """bf16_prefill_chunk512_x8 through mlr_paged_prefill (varlen, one launch
     per call). The call passes the reference's tile_size (64); it only orders
     the FP32 accumulation, and the matrix-core kernel steps by its own 64-key
     tile whatever it is, so there is one timing: the median over `reps`
-    bracketed replays of a graph of `calls_per_graph` calls."""
+    bracketed replays of a graph of `calls_per_graph` calls. `dtype` runs the
+    same inputs cast to another type (fp16)."""
     import torch
 
     from mini_llm_runtime_amd import workloads
@@ -542,8 +543,9 @@ def bench_prefill(device, reps=5, calls_per_graph=10):
     kc, vc = wl.k_cache.clone(), wl.v_cache.clone()
     kc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_k)
     vc.view(-1, 2, 64).index_copy_(0, wl.slot_mapping, wl.chunk_v)
-    kc, vc = kc.to(device), vc.to(device)
-    q = wl.q.to(device)
+    dtype = dtype or wl.q.dtype
+    kc, vc = kc.to(device, dtype), vc.to(device, dtype)
+    q = wl.q.to(device, dtype)
     bt, qsl, ctx = (t.to(device) for t in (wl.block_tables, wl.query_start_loc,
                                             wl.context_lens))
     out = torch.empty_like(q)
@@ -1461,6 +1463,12 @@ def main():
             "sclk_mhz": pre["sclk"],
             "cpu_baseline": cpu_pre,
         }
+        pre16 = bench_prefill(device, dtype=torch.float16)
+        line["prefill"]["fp16"] = {
+            "what": "the same call with q and the cache in fp16 (fp16 matrix-core operands)",
+            "us_per_call": pre16["us_per_call"],
+            "tflops": round(pre16["tflops"], 3),
+            "frac_of_fp16_peak": round(pre16["tflops"] / BF16_PEAK_TFLOPS, 5)}
     line["fp32_decode_b4"] = bench_fp32_decode_b4(
         device, 0 if args.no_cpu_baseline else args.cpu_budget / 4)
     if not args.no_pre_attention:
