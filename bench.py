@@ -39,17 +39,18 @@ request, 32 q / 8 KV heads, head_dim 128, 512 to 16384 tokens, bf16 and fp16)
 beside its published latencies; ``decode_runtime``, the reference's own
 full-model batched decode-step cases (Qwen2.5-0.5B shape, B=8 at contexts
 288..512 and B=16 at 128, BF16 and FP32), eager and replayed from a HIP graph,
-beside its published step times; and ``serving`` / ``serving_decode_graphs``,
+beside its published step times; and ``serving`` / ``serving_graphs``,
 end-to-end continuous-batching steps of a random-init Qwen2.5-0.5B-shape model
 in BF16 (workloads.qwen05b_serving: about 48 decodes + 2 x 1024-token
 prefills per step, 128 steps after the warm-up), eager and with the decode
-forward replayed from HIP graphs. ``provenance`` names the sources and
+forward and repeated packed prefills replayed from HIP graphs. ``provenance`` names the sources and
 library the numbers come from.
 
     python bench.py [--gpus 1] [--steps 240] [--warmup 48]
 
-``--serving`` runs only the serving steps (eager; with ``--decode-graphs``,
-the decode forward replayed from HIP graphs) and prints their line.
+``--serving`` runs only the serving steps (eager; with ``--graphs``, the
+decode forward and repeated prefills replayed from HIP graphs) and prints
+their line.
 
 ``--profile`` launches the same kernels eagerly and untimed, for rocprofv3:
 ``--steps`` decode steps over the rotated layers, one decode without the
@@ -99,8 +100,9 @@ def parse_args():
                    help="launch the kernels eagerly, untimed (for rocprofv3)")
     p.add_argument("--serving", action="store_true",
                    help="time only the end-to-end serving steps (qwen05b_serving, BF16)")
-    p.add_argument("--decode-graphs", action="store_true",
-                   help="with --serving: replay each step's decode forward from HIP graphs")
+    p.add_argument("--graphs", action="store_true",
+                   help="with --serving: replay the decode forward, and repeated packed "
+                        "prefills, from HIP graphs")
     p.add_argument("--no-serving", action="store_true",
                    help="leave the serving steps out of the default run")
     p.add_argument("--no-contiguous", action="store_true",
@@ -905,7 +907,7 @@ def bench_decode_runtime(device, warmup=10, samples=50):
     slots on every call. Random-init weights (no checkpoint here); the step's
     time does not depend on their values. Each case is timed twice: the eager
     forward (as the reference runs it) and the same step replayed from a HIP
-    graph (runtime/decode_graphs.py: the metadata checks with one host sync,
+    graph (runtime/step_graphs.py: the metadata checks with one host sync,
     the input copies and the replay, inside the timed call). Every timed
     call's logits must be finite."""
     import math
@@ -913,7 +915,7 @@ def bench_decode_runtime(device, warmup=10, samples=50):
     import torch
 
     from mini_llm_runtime_amd.model.qwen2 import TinyQwen2Config, TinyQwen2ForCausalLM
-    from mini_llm_runtime_amd.runtime.decode_graphs import DecodeGraphs
+    from mini_llm_runtime_amd.runtime.step_graphs import DecodeGraphs
     from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
     from mini_llm_runtime_amd.workloads import QWEN05B_CONFIG
 
@@ -1194,18 +1196,20 @@ def cpu_baseline_prefill(wl, budget):
     }
 
 
-def bench_serving(device, steps=None, decode_graphs=False):
+def bench_serving(device, steps=None, graphs=False):
     """End-to-end continuous-batching steps at Qwen2.5-0.5B shape in BF16
     (workloads.qwen05b_serving): schedule, pack, 24-layer forward on the HIP
     attention kernels with PyTorch GEMMs, sample, update. After the warm-up
     (all 48 initial prompts admitted), each step is timed on the host with a
     device synchronisation on both sides. Every timed step's logits must be
     finite (checked after the loop; the merge-failure flag is checked inside
-    each step). decode_graphs: each step's decodes replay the batched decode
-    forward from a HIP graph per batch size (runtime/decode_graphs.py), block
-    tables padded to the workload's longest request; the graphs of every batch
-    size up to the scheduler's max_num_seqs are recorded before the warm-up
-    (their recording time is reported, outside the steps)."""
+    each step). graphs: each step's decodes replay the batched decode forward
+    from a HIP graph per batch size (runtime/step_graphs.py: DecodeGraphs),
+    block tables padded to the workload's longest request, and packed
+    prefills whose shape repeats replay theirs (PrefillGraphs: recorded the
+    third time a shape is met, the eight most recent kept); the decode graphs
+    of every batch size up to the scheduler's max_num_seqs are recorded before
+    the warm-up (their recording time is reported, outside the steps)."""
     import torch
 
     from mini_llm_runtime_amd import workloads
@@ -1214,26 +1218,28 @@ def bench_serving(device, steps=None, decode_graphs=False):
     w = workloads.qwen05b_serving()
     steps = steps or w.steps
     _, model, cache, scheduler, _ = workloads.build_serving(w, device, torch.bfloat16)
-    graphs = None
-    if decode_graphs:
-        from mini_llm_runtime_amd.runtime.decode_graphs import DecodeGraphs
+    dgraphs = pgraphs = None
+    if graphs:
+        from mini_llm_runtime_amd.runtime.step_graphs import DecodeGraphs, PrefillGraphs
 
         longest = max(len(p) + m for p, m in w.initial + w.arrivals)
-        graphs = DecodeGraphs(model, cache, max_blocks_per_seq=-(-longest // w.block_size))
+        dgraphs = DecodeGraphs(model, cache, max_blocks_per_seq=-(-longest // w.block_size))
+        pgraphs = PrefillGraphs(model, cache)
         t0 = time.perf_counter()
         with torch.no_grad():
-            graphs.record(range(1, w.max_num_seqs + 1))
+            dgraphs.record(range(1, w.max_num_seqs + 1))
         torch.cuda.synchronize()
         record_s = time.perf_counter() - t0
     times, decode_tokens, prefill_tokens, finished = [], 0, 0, 0
     with torch.no_grad():
         warm = workloads.serving_warm_up(model, scheduler, len(w.initial),
-                                         decode_graphs=graphs)
+                                         decode_graphs=dgraphs, prefill_graphs=pgraphs)
         finite = []  # per step, read after the timed loop
         for _ in range(steps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            result = run_generation_step(model, scheduler, decode_graphs=graphs)
+            result = run_generation_step(model, scheduler, decode_graphs=dgraphs,
+                                         prefill_graphs=pgraphs)
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t0)
             finite.append(torch.isfinite(result.packed_logits).all())
@@ -1278,10 +1284,13 @@ def bench_serving(device, steps=None, decode_graphs=False):
         "tokens_per_s": round((decode_tokens + prefill_tokens) / total, 1),
         "decode_tokens_per_s": round(decode_tokens / total, 1),
         "requests_finished": finished,
-        "decode_graphs": (None if graphs is None else
-                          {"recorded": graphs.captures, "record_s": round(record_s, 2),
-                           "replays": graphs.replays, "eager_calls": graphs.eager_calls,
-                           "max_blocks_per_seq": graphs.width}),
+        "decode_graphs": (None if dgraphs is None else
+                          {"recorded": dgraphs.captures, "record_s": round(record_s, 2),
+                           "replays": dgraphs.replays, "eager_calls": dgraphs.eager_calls,
+                           "max_blocks_per_seq": dgraphs.width}),
+        "prefill_graphs": (None if pgraphs is None else
+                           {"recorded": pgraphs.captures, "replays": pgraphs.replays,
+                            "eager_calls": pgraphs.eager_calls}),
     }
 
 
@@ -1379,7 +1388,7 @@ def main():
         return
     if args.serving:
         print(json.dumps({"metric": "serving step (qwen05b_serving, bf16)",
-                          **bench_serving(device, decode_graphs=args.decode_graphs)}),
+                          **bench_serving(device, graphs=args.graphs)}),
               flush=True)
         return
     dec = bench_decode(args, device)
@@ -1483,7 +1492,7 @@ def main():
     line["decode_runtime"] = bench_decode_runtime(device)
     if not args.no_serving:
         line["serving"] = bench_serving(device)
-        line["serving_decode_graphs"] = bench_serving(device, decode_graphs=True)
+        line["serving_graphs"] = bench_serving(device, graphs=True)
     print(json.dumps(line), flush=True)
 
 

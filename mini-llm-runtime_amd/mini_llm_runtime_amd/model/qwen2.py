@@ -321,7 +321,7 @@ class TinyQwen2Model(nn.Module):
         checks on these position, slot, block-table and length tensors against
         this cache (Qwen2Attention._check_decode_metadata), so no layer runs
         them and the call makes no host sync; the HIP-graph decode
-        (runtime/decode_graphs.py) checks before it copies its inputs in."""
+        (runtime/step_graphs.py) checks before it copies its inputs in."""
         if input_ids.ndim != 2 or input_ids.shape[1] != 1:
             raise ValueError("input_ids must have shape [B, 1] for decode")
         if input_ids.shape[0] == 0:
@@ -352,14 +352,36 @@ class TinyQwen2Model(nn.Module):
                                           block_tables: torch.Tensor,
                                           query_start_loc: torch.Tensor,
                                           context_lens: torch.Tensor,
-                                          max_query_len: int) -> torch.Tensor:
+                                          max_query_len: int, *,
+                                          metadata_checked: bool = False) -> torch.Tensor:
         """Packed prefill of R requests: [T] token ids -> [T, hidden_size].
 
         Request r owns tokens query_start_loc[r]:query_start_loc[r+1]
         (non-empty), at positions context_lens[r] - len_r .. context_lens[r] - 1
         of its block table (a whole prompt when the prefix is 0, else a chunk
         after a cached prefix). The metadata is checked once here, on the
-        device with one host sync, before any layer writes the cache."""
+        device with one host sync, before any layer writes the cache.
+
+        metadata_checked: the caller already ran these checks
+        (check_prefill_packed_inputs) on these tensors, so the call makes no
+        host sync; the HIP-graph prefill (runtime/step_graphs.py) does."""
+        if not metadata_checked:
+            self.check_prefill_packed_inputs(input_ids, position_ids, kv_cache, slot_mapping,
+                                             block_tables, query_start_loc, context_lens,
+                                             max_query_len)
+        hidden_states = self.embed_tokens(input_ids)
+        for layer_idx, layer in enumerate(self.layers):
+            hidden_states = layer.forward_prefill_packed_with_cache(
+                hidden_states, position_ids, kv_cache, layer_idx, slot_mapping, block_tables,
+                query_start_loc, context_lens, max_query_len)
+        return self.norm(hidden_states)
+
+    def check_prefill_packed_inputs(self, input_ids, position_ids, kv_cache, slot_mapping,
+                                    block_tables, query_start_loc, context_lens,
+                                    max_query_len) -> None:
+        """The checks of forward_prefill_packed_with_cache: shapes, dtypes,
+        devices and the cache first, then the metadata on the device (one host
+        sync); raises before anything is written."""
         if input_ids.ndim != 1 or input_ids.shape[0] == 0:
             raise ValueError("input_ids must have shape [num_tokens] with num_tokens > 0")
         self._check_ids(input_ids)
@@ -385,12 +407,6 @@ class TinyQwen2Model(nn.Module):
         self._check_packed_metadata(kv_cache, position_ids, slot_mapping, block_tables,
                                     query_start_loc, context_lens, max_query_len,
                                     input_ids.shape[0])
-        hidden_states = self.embed_tokens(input_ids)
-        for layer_idx, layer in enumerate(self.layers):
-            hidden_states = layer.forward_prefill_packed_with_cache(
-                hidden_states, position_ids, kv_cache, layer_idx, slot_mapping, block_tables,
-                query_start_loc, context_lens, max_query_len)
-        return self.norm(hidden_states)
 
     @staticmethod
     def _check_packed_metadata(kv_cache, position_ids, slot_mapping, block_tables,
@@ -476,8 +492,9 @@ class TinyQwen2ForCausalLM(nn.Module):
 
     def forward_prefill_packed_with_cache(self, input_ids, position_ids, kv_cache,
                                           slot_mapping, block_tables, query_start_loc,
-                                          context_lens, max_query_len) -> torch.Tensor:
+                                          context_lens, max_query_len, *,
+                                          metadata_checked: bool = False) -> torch.Tensor:
         """[T] -> [T, vocab_size] logits for the packed prefill tokens."""
         return self.lm_head(self.model.forward_prefill_packed_with_cache(
             input_ids, position_ids, kv_cache, slot_mapping, block_tables, query_start_loc,
-            context_lens, max_query_len))
+            context_lens, max_query_len, metadata_checked=metadata_checked))

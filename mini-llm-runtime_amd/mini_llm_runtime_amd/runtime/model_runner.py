@@ -15,9 +15,10 @@ whatever the order of phases in the batch. The batch checks are the
 reference's, with its messages and order, evaluated with two host syncs
 instead of several per request.
 
-With ``decode_graphs`` (runtime/decode_graphs.py) the decodes of a step
+With ``decode_graphs`` (runtime/step_graphs.py) the decodes of a step
 replay a HIP graph of the batched decode forward, recorded once per batch
-size, instead of issuing its kernels from the host.
+size, instead of issuing its kernels from the host; with ``prefill_graphs``
+a packed prefill whose shape repeats replays its recorded forward.
 
 ``run_generation_step`` also checks the decode workspaces once per step: a
 split merge that gave up waiting (it only writes NaN) raises
@@ -275,16 +276,17 @@ def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list
 
 
 def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
-                        decode_graphs=None) -> torch.Tensor:
+                        decode_graphs=None, prefill_graphs=None) -> torch.Tensor:
     """[num_packed_tokens, vocab_size] logits in packed token order.
 
-    decode_graphs: a DecodeGraphs (runtime/decode_graphs.py) of this model and
-    cache; the batch's decodes then replay its recorded step instead of
-    running the decode forward eagerly."""
+    decode_graphs / prefill_graphs: a DecodeGraphs / PrefillGraphs
+    (runtime/step_graphs.py) of this model and cache; the batch's decodes
+    (prefills) then go through it, replaying recorded graphs instead of
+    running the forward eagerly."""
     qsl, num_tokens = _check_batch(model, batch, kv_cache)
-    if decode_graphs is not None and (decode_graphs.model is not model
-                                      or decode_graphs.kv_cache is not kv_cache):
-        raise ValueError("decode_graphs must belong to this model and KV cache")
+    for name, graphs in (("decode_graphs", decode_graphs), ("prefill_graphs", prefill_graphs)):
+        if graphs is not None and (graphs.model is not model or graphs.kv_cache is not kv_cache):
+            raise ValueError(f"{name} must belong to this model and KV cache")
     device = batch.input_token_ids.device
     logits = model.lm_head.weight.new_empty((num_tokens, model.lm_head.out_features))
     prefill = [i for i, ph in enumerate(batch.request_phases) if ph is RequestStatus.PREFILLING]
@@ -303,11 +305,15 @@ def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
         offsets = [0]
         for n in lens:
             offsets.append(offsets[-1] + n)
-        out = model.forward_prefill_packed_with_cache(
-            pick(batch.input_token_ids), pick(batch.positions), kv_cache,
-            pick(batch.slot_mapping), batch.block_tables.index_select(0, req),
-            torch.tensor(offsets, dtype=torch.long, device=device),
-            batch.context_lens.index_select(0, req), max(lens))
+        packed = (pick(batch.input_token_ids), pick(batch.positions), pick(batch.slot_mapping),
+                  batch.block_tables.index_select(0, req),
+                  torch.tensor(offsets, dtype=torch.long, device=device),
+                  batch.context_lens.index_select(0, req))
+        if prefill_graphs is not None:
+            out = prefill_graphs(*packed, max(lens))
+        else:
+            out = model.forward_prefill_packed_with_cache(*packed[:2], kv_cache, *packed[2:],
+                                                          max(lens))
         if contiguous:
             logits[rows] = out
         else:
@@ -351,7 +357,7 @@ def greedy_sample(packed_logits: torch.Tensor, batch: ModelBatch) -> dict[str, i
 
 def run_generation_step(model, scheduler: Scheduler,
                         eos_token_id: int | None = None,
-                        decode_graphs=None) -> GenerationStepResult:
+                        decode_graphs=None, prefill_graphs=None) -> GenerationStepResult:
     if not scheduler.waiting and not scheduler.running:
         raise ValueError("Cannot run generation step with no requests")
     scheduler_output = scheduler.schedule()
@@ -360,7 +366,8 @@ def run_generation_step(model, scheduler: Scheduler,
     batch = build_model_batch(scheduler_output, block_size=scheduler.kv_cache.block_size,
                               device=scheduler.kv_cache.device)
     packed_logits = execute_model_batch(model=model, batch=batch, kv_cache=scheduler.kv_cache,
-                                        decode_graphs=decode_graphs)
+                                        decode_graphs=decode_graphs,
+                                        prefill_graphs=prefill_graphs)
     sampled = greedy_sample(packed_logits, batch)
     if batch.input_token_ids.device.type == "cuda":
         # Before any sampled token is committed to the scheduler.
@@ -377,10 +384,11 @@ def run_generation_step(model, scheduler: Scheduler,
 
 def run_greedy_generation(model, scheduler: Scheduler,
                           eos_token_id: int | None = None,
-                          decode_graphs=None) -> list[Request]:
+                          decode_graphs=None, prefill_graphs=None) -> list[Request]:
     """Schedule-model-sample-update until every request has finished."""
     finished: list[Request] = []
     while scheduler.waiting or scheduler.running:
-        finished.extend(run_generation_step(model, scheduler, eos_token_id=eos_token_id,
-                                            decode_graphs=decode_graphs).finished_requests)
+        finished.extend(run_generation_step(
+            model, scheduler, eos_token_id=eos_token_id, decode_graphs=decode_graphs,
+            prefill_graphs=prefill_graphs).finished_requests)
     return finished

@@ -1,4 +1,5 @@
-"""The batched decode step of a causal LM replayed from HIP graphs.
+"""The batched decode step, and repeated packed prefills, of a causal LM
+replayed from HIP graphs.
 
 The reference runs every decode step eagerly
 (runtime/model_runner.py:execute_model_batch ->
@@ -43,9 +44,26 @@ recorded: replace a weight or the cache and call ``reset()``. Replays must not
 overlap (one stream at a time): the graphs of one runner share its decode
 workspace. A block table wider than ``max_blocks_per_seq`` runs the same step
 eagerly (counted in ``eager_calls``).
+
+``PrefillGraphs`` does the same for the packed prefill forward
+(``forward_prefill_packed_with_cache``, logits of every packed token), whose
+shape a server meets again and again (the same number of prompts of the same
+lengths each step). A graph is keyed by the call's shape: tokens, requests,
+longest query and block-table width (the prefill launch's grid follows from
+them; the offsets, lengths, slots and tables are read on the device). A shape
+runs eagerly until it is met for the ``record_at``-th time, and is recorded
+then; at most ``max_graphs`` recordings are kept (least recently used
+dropped), as each holds its logits buffer ([tokens, vocab]). Only a runner's
+first recording runs the eager step before its capture: the packed prefill
+uses no decode workspace, and the model's cached weights and the stream's
+GEMM state exist from then on. Every call runs the model's
+own checks first (``check_prefill_packed_inputs``: one host sync, before
+anything is written).
 """
 
 from __future__ import annotations
+
+from collections import OrderedDict
 
 import torch
 
@@ -76,6 +94,41 @@ class _Recorded:
             self.block_tables[:, width:].fill_(-1)
 
 
+def _record(device, stream, step, warm=True):
+    """With `warm`, one eager `step` on `stream` first (it sizes that stream's
+    cached decode workspace and builds the model's concatenated weights and
+    the stream's GEMM state outside the graph); then `step` recorded on
+    `stream`: (graph, its output)."""
+    current = torch.cuda.current_stream(device)
+    stream.wait_stream(current)
+    if warm:
+        with torch.cuda.stream(stream):
+            step()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = step()
+    current.wait_stream(stream)
+    return graph, out
+
+
+def _check_pair(model, kv_cache) -> torch.device:
+    device = kv_cache.device
+    if device.type != "cuda":
+        raise ValueError("step graphs need the KV cache on a HIP device")
+    if model.lm_head.weight.device != device:
+        raise ValueError("model and KV cache must be on the same device")
+    config = model.model.config
+    if kv_cache.num_layers != config.num_hidden_layers:
+        raise ValueError("KV cache num_layers must match model layers")
+    if kv_cache.num_kv_heads != config.num_key_value_heads:
+        raise ValueError("KV cache num_kv_heads must match model num_key_value_heads")
+    if kv_cache.head_dim != config.head_dim:
+        raise ValueError("KV cache head_dim must match model head_dim")
+    if kv_cache.dtype != model.lm_head.weight.dtype:
+        raise ValueError("KV cache dtype must match the model's dtype")
+    return device
+
+
 class DecodeGraphs:
     """HIP-graph replay of ``model.forward_decode_batch_with_cache`` on one
     paged KV cache (see the module docstring).
@@ -87,20 +140,7 @@ class DecodeGraphs:
     """
 
     def __init__(self, model, kv_cache: PagedKVCache, max_blocks_per_seq: int) -> None:
-        device = kv_cache.device
-        if device.type != "cuda":
-            raise ValueError("DecodeGraphs needs the KV cache on a HIP device")
-        if model.lm_head.weight.device != device:
-            raise ValueError("model and KV cache must be on the same device")
-        config = model.model.config
-        if kv_cache.num_layers != config.num_hidden_layers:
-            raise ValueError("KV cache num_layers must match model layers")
-        if kv_cache.num_kv_heads != config.num_key_value_heads:
-            raise ValueError("KV cache num_kv_heads must match model num_key_value_heads")
-        if kv_cache.head_dim != config.head_dim:
-            raise ValueError("KV cache head_dim must match model head_dim")
-        if kv_cache.dtype != model.lm_head.weight.dtype:
-            raise ValueError("KV cache dtype must match the model's dtype")
+        device = _check_pair(model, kv_cache)
         if int(max_blocks_per_seq) <= 0:
             raise ValueError("max_blocks_per_seq must be > 0")
         self.model = model
@@ -182,15 +222,7 @@ class DecodeGraphs:
             r.context_lens, metadata_checked=True)
 
     def _record(self, r: _Recorded) -> None:
-        current = torch.cuda.current_stream(self.device)
-        self.stream.wait_stream(current)
-        with torch.cuda.stream(self.stream):
-            self._step(r)  # eager: sizes this stream's decode workspace
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=self.stream):
-            r.logits = self._step(r)
-        current.wait_stream(self.stream)
-        r.graph = graph
+        r.graph, r.logits = _record(self.device, self.stream, lambda: self._step(r))
         self.captures += 1
 
     def __call__(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
@@ -214,6 +246,107 @@ class DecodeGraphs:
             self._recorded[batch] = r
         else:
             r.load(input_ids, position_ids, slot_mapping, block_tables, context_lens)
+        r.graph.replay()
+        self.replays += 1
+        return r.logits
+
+
+class _PrefillRecorded:
+    """Static inputs of one prefill shape and its graph."""
+
+    def __init__(self, tokens: int, requests: int, width: int, device: torch.device) -> None:
+        def zeros(*shape):
+            return torch.zeros(*shape, dtype=torch.long, device=device)
+
+        self.input_ids = zeros(tokens)
+        self.position_ids = zeros(tokens)
+        self.slot_mapping = zeros(tokens)
+        self.block_tables = zeros(requests, width)
+        self.query_start_loc = zeros(requests + 1)
+        self.context_lens = zeros(requests)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.logits: torch.Tensor | None = None
+
+    def load(self, input_ids, position_ids, slot_mapping, block_tables, query_start_loc,
+             context_lens) -> None:
+        self.input_ids.copy_(input_ids)
+        self.position_ids.copy_(position_ids)
+        self.slot_mapping.copy_(slot_mapping)
+        self.block_tables.copy_(block_tables)
+        self.query_start_loc.copy_(query_start_loc)
+        self.context_lens.copy_(context_lens)
+
+
+class PrefillGraphs:
+    """HIP-graph replay of ``model.forward_prefill_packed_with_cache`` for
+    shapes met more than once (see the module docstring).
+
+    model: a TinyQwen2ForCausalLM on a HIP device, in eval mode.
+    kv_cache: the PagedKVCache the prefills write.
+    max_graphs: recordings kept at once (least recently used dropped).
+    record_at: the sighting of a shape that records it (1: the first).
+    """
+
+    def __init__(self, model, kv_cache: PagedKVCache, max_graphs: int = 8,
+                 record_at: int = 3) -> None:
+        self.device = _check_pair(model, kv_cache)
+        if int(max_graphs) <= 0 or int(record_at) <= 0:
+            raise ValueError("max_graphs and record_at must be > 0")
+        self.record_at = int(record_at)
+        self._warmed = False
+        self.model = model
+        self.kv_cache = kv_cache
+        self.max_graphs = int(max_graphs)
+        self.stream = torch.cuda.Stream(self.device)  # default priority
+        self._recorded: OrderedDict[tuple, _PrefillRecorded] = OrderedDict()
+        self._seen: dict[tuple, int] = {}
+        self.captures = 0
+        self.replays = 0
+        self.eager_calls = 0
+
+    def reset(self) -> None:
+        """Drop every recorded graph (after a weight or the cache changed)."""
+        self._recorded.clear()
+        self._seen.clear()
+
+    def __call__(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
+                 slot_mapping: torch.Tensor, block_tables: torch.Tensor,
+                 query_start_loc: torch.Tensor, context_lens: torch.Tensor,
+                 max_query_len: int) -> torch.Tensor:
+        """[T] token ids -> [T, vocab_size] logits (for a replay, the graph's
+        output buffer, valid until that shape's next replay)."""
+        self.model.model.check_prefill_packed_inputs(
+            input_ids, position_ids, self.kv_cache, slot_mapping, block_tables,
+            query_start_loc, context_lens, max_query_len)
+        key = (input_ids.shape[0], context_lens.shape[0], int(max_query_len),
+               block_tables.shape[1])
+        args = (input_ids, position_ids, slot_mapping, block_tables, query_start_loc,
+                context_lens)
+        r = self._recorded.get(key)
+        if r is None:
+            seen = self._seen.get(key, 0) + 1
+            if len(self._seen) >= 4096:
+                self._seen.clear()
+            self._seen[key] = seen
+            if seen < self.record_at:
+                self.eager_calls += 1
+                return self.model.forward_prefill_packed_with_cache(
+                    *args[:2], self.kv_cache, *args[2:], max_query_len, metadata_checked=True)
+            r = _PrefillRecorded(key[0], key[1], key[3], self.device)
+            r.load(*args)
+            r.graph, r.logits = _record(self.device, self.stream, lambda: (
+                self.model.forward_prefill_packed_with_cache(
+                    r.input_ids, r.position_ids, self.kv_cache, r.slot_mapping,
+                    r.block_tables, r.query_start_loc, r.context_lens, key[2],
+                    metadata_checked=True)), warm=not self._warmed)
+            self._warmed = True
+            self.captures += 1
+            self._recorded[key] = r
+            while len(self._recorded) > self.max_graphs:
+                self._recorded.popitem(last=False)
+        else:
+            self._recorded.move_to_end(key)
+            r.load(*args)
         r.graph.replay()
         self.replays += 1
         return r.logits

@@ -265,14 +265,15 @@ def build_serving(w: ServingWorkload, device, dtype):
 
 
 def serving_warm_up(model, scheduler, num_initial: int, max_steps: int = 1000,
-                    decode_graphs=None) -> int:
+                    decode_graphs=None, prefill_graphs=None) -> int:
     """Run steps until every initial request has been admitted; returns the
     number of steps run."""
     from .runtime.model_runner import run_generation_step
 
     steps = 0
     while any(r.request_id.startswith("init") for r in scheduler.waiting):
-        run_generation_step(model, scheduler, decode_graphs=decode_graphs)
+        run_generation_step(model, scheduler, decode_graphs=decode_graphs,
+                            prefill_graphs=prefill_graphs)
         steps += 1
         if steps > max_steps:
             raise RuntimeError("warm-up did not admit the initial requests")

@@ -1,5 +1,5 @@
-"""The batched decode step replayed from HIP graphs (runtime/decode_graphs.py)
-against the same step run eagerly.
+"""The batched decode step and repeated packed prefills replayed from HIP
+graphs (runtime/step_graphs.py) against the same calls run eagerly.
 
 An eager step given the block table padded to the runner's width launches the
 same kernels with the same grids as the replay, so the two must agree bit for
@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from mini_llm_runtime_amd.model.qwen2 import TinyQwen2Config, TinyQwen2ForCausalLM
-from mini_llm_runtime_amd.runtime.decode_graphs import DecodeGraphs
+from mini_llm_runtime_amd.runtime.step_graphs import DecodeGraphs, PrefillGraphs
 from mini_llm_runtime_amd.runtime.model_runner import run_greedy_generation
 from mini_llm_runtime_amd.runtime.paged_kv_cache import PagedKVCache
 from mini_llm_runtime_amd.runtime.request import Request
@@ -164,24 +164,27 @@ def test_wider_table_than_recorded_runs_eagerly(device):
     assert torch.equal(cache_g.k_cache, cache_e.k_cache)
 
 
-def _serve(device, dtype, with_graphs, record_ahead=False):
+def _serve(device, dtype, with_graphs, record_ahead=False, prefill=False, prompt_len=None):
     model = _model(device, dtype, seed=11)
     cache = PagedKVCache(2, NBLOCKS, BS, 2, 64, dtype=dtype, device=device)
     scheduler = Scheduler(max_num_batched_tokens=512, max_num_seqs=8, kv_cache=cache)
     gen = torch.Generator().manual_seed(12)
     requests = []
     for i in range(10):
-        n = int(torch.randint(3, 200, (1,), generator=gen))
+        n = prompt_len or int(torch.randint(3, 200, (1,), generator=gen))
         prompt = torch.randint(0, QWEN_2L["vocab_size"], (n,), generator=gen).tolist()
         requests.append(Request(f"r{i}", prompt, int(torch.randint(4, 24, (1,), generator=gen)),
                                 float(i)))
     for r in requests:
         scheduler.add_request(r)
     graphs = DecodeGraphs(model, cache, max_blocks_per_seq=WIDTH) if with_graphs else None
+    pgraphs = PrefillGraphs(model, cache, record_at=2) if prefill else None
     with torch.no_grad():
         if record_ahead:
             graphs.record(range(1, 9))
-        run_greedy_generation(model, scheduler, decode_graphs=graphs)
+        run_greedy_generation(model, scheduler, decode_graphs=graphs, prefill_graphs=pgraphs)
+    if prefill:
+        return {r.request_id: r.output_token_ids for r in requests}, pgraphs
     return {r.request_id: r.output_token_ids for r in requests}, graphs
 
 
@@ -209,3 +212,102 @@ def test_recorded_ahead_serving_records_nothing_more(device):
     free = len(cache.free_blocks)
     graphs.release()
     assert len(cache.free_blocks) == free + held
+
+
+def _prefill_step(device, qlens, prefixes, gen):
+    """One packed prefill of len(qlens) requests on distinct random blocks:
+    request r's chunk is positions prefixes[r] .. prefixes[r] + qlens[r] - 1."""
+    ctxs = [p + n for p, n in zip(prefixes, qlens)]
+    perm = torch.randperm(NBLOCKS, generator=gen).tolist()
+    tables, used = [], 0
+    for c in ctxs:
+        nb = -(-c // BS)
+        tables.append(perm[used:used + nb])
+        used += nb
+    width = max(map(len, tables))
+    pos = torch.cat([torch.arange(p, p + n) for p, n in zip(prefixes, qlens)])
+    owner = torch.cat([torch.full((n,), r) for r, n in enumerate(qlens)])
+    slots = torch.tensor([tables[r][int(t) // BS] * BS + int(t) % BS
+                          for r, t in zip(owner.tolist(), pos.tolist())])
+    qsl = torch.tensor([0] + torch.tensor(qlens).cumsum(0).tolist())
+    step = dict(input_ids=torch.randint(0, QWEN_2L["vocab_size"], (len(pos),), generator=gen),
+                position_ids=pos, slot_mapping=slots,
+                block_tables=torch.tensor([t + [-1] * (width - len(t)) for t in tables]),
+                query_start_loc=qsl, context_lens=torch.tensor(ctxs))
+    return {k: v.to(device) for k, v in step.items()}, max(qlens)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("prefixes", [[0, 0], [100, 7]], ids=["prompts", "chunks"])
+def test_prefill_replays_equal_the_eager_forward(device, dtype, prefixes):
+    """Four packed prefills of one shape (two requests of 64 and 130 tokens),
+    recorded on the second: the first runs eagerly, all four equal the eager
+    forward bit for bit (logits and K/V), with eager work between calls."""
+    model = _model(device, dtype)
+    cache_g, cache_e = _cache(device, dtype), _cache(device, dtype)
+    graphs = PrefillGraphs(model, cache_g, record_at=2)
+    gen = torch.Generator().manual_seed(21)
+    with torch.no_grad():
+        for i in range(4):
+            step, max_q = _prefill_step(device, [64, 130], prefixes, gen)
+            want = model.forward_prefill_packed_with_cache(
+                step["input_ids"], step["position_ids"], cache_e, step["slot_mapping"],
+                step["block_tables"], step["query_start_loc"], step["context_lens"], max_q)
+            torch.cuda.synchronize()
+            other = torch.randn(1 << 20, device=device).square().sum()
+            got = graphs(**step, max_query_len=max_q).clone()
+            torch.cuda.synchronize()
+            assert torch.isfinite(other)
+            assert torch.equal(got, want), f"call {i}"
+            assert torch.equal(cache_g.k_cache, cache_e.k_cache), f"call {i}"
+            assert torch.equal(cache_g.v_cache, cache_e.v_cache), f"call {i}"
+    assert (graphs.eager_calls, graphs.captures, graphs.replays) == (1, 1, 3)
+
+
+def test_prefill_graphs_keep_the_most_recent_shapes(device):
+    """With max_graphs=1 two alternating shapes keep replacing each other's
+    recording; results stay equal to the eager forward."""
+    model = _model(device, torch.bfloat16)
+    cache_g, cache_e = _cache(device, torch.bfloat16), _cache(device, torch.bfloat16)
+    graphs = PrefillGraphs(model, cache_g, max_graphs=1, record_at=2)
+    gen = torch.Generator().manual_seed(22)
+    with torch.no_grad():
+        for i in range(6):
+            qlens = [32, 50] if i % 2 == 0 else [17]
+            step, max_q = _prefill_step(device, qlens, [0] * len(qlens), gen)
+            want = model.forward_prefill_packed_with_cache(
+                step["input_ids"], step["position_ids"], cache_e, step["slot_mapping"],
+                step["block_tables"], step["query_start_loc"], step["context_lens"], max_q)
+            assert torch.equal(graphs(**step, max_query_len=max_q), want), f"call {i}"
+    assert len(graphs._recorded) == 1
+    assert graphs.eager_calls == 2 and graphs.captures == 4
+
+
+def test_prefill_bad_metadata_is_refused_before_anything_is_written(device):
+    model, cache = _model(device, torch.bfloat16), _cache(device, torch.bfloat16)
+    graphs = PrefillGraphs(model, cache, record_at=1)
+    gen = torch.Generator().manual_seed(23)
+    with torch.no_grad():
+        for _ in range(2):  # recorded
+            step, max_q = _prefill_step(device, [40, 41], [0, 0], gen)
+            graphs(**step, max_query_len=max_q)
+        step, max_q = _prefill_step(device, [40, 41], [0, 0], gen)
+        step["slot_mapping"] = step["slot_mapping"].clone()
+        step["slot_mapping"][3] += 1
+        k0, v0 = cache.k_cache.clone(), cache.v_cache.clone()
+        replays = graphs.replays
+        with pytest.raises(ValueError, match="slot"):
+            graphs(**step, max_query_len=max_q)
+        torch.cuda.synchronize()
+    assert graphs.replays == replays
+    assert torch.equal(cache.k_cache, k0) and torch.equal(cache.v_cache, v0)
+
+
+def test_serving_with_prefill_and_decode_graphs_gives_the_eager_tokens(device):
+    """FP32 continuous batching with prompts of one length (so packed prefill
+    shapes repeat) and both kinds of graphs: the eager run's tokens."""
+    eager, _ = _serve(device, torch.float32, with_graphs=False, prompt_len=48)
+    replayed, pgraphs = _serve(device, torch.float32, with_graphs=True, prefill=True,
+                               prompt_len=48)
+    assert replayed == eager
+    assert pgraphs.replays > 0

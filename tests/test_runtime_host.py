@@ -303,17 +303,19 @@ def test_serving_schedule_block_tables_match_oracle_allocator():
     assert steps_with_prefill > 50
 
 
-def test_decode_graphs_need_a_hip_cache(tiny_cpu):
-    """The HIP-graph decode refuses a cache that is not on a HIP device."""
-    from mini_llm_runtime_amd.runtime.decode_graphs import DecodeGraphs
+def test_step_graphs_need_a_hip_cache(tiny_cpu):
+    """The HIP-graph decode and prefill refuse a cache not on a HIP device."""
+    from mini_llm_runtime_amd.runtime.step_graphs import DecodeGraphs, PrefillGraphs
 
     model, cache = tiny_cpu
-    with pytest.raises(ValueError, match="needs the KV cache on a HIP device"):
+    with pytest.raises(ValueError, match="need the KV cache on a HIP device"):
         DecodeGraphs(model, cache, max_blocks_per_seq=4)
+    with pytest.raises(ValueError, match="need the KV cache on a HIP device"):
+        PrefillGraphs(model, cache)
 
 
-def test_execute_model_batch_refuses_foreign_decode_graphs(tiny_cpu):
-    """decode_graphs of another model or cache is refused before any launch."""
+def test_execute_model_batch_refuses_foreign_step_graphs(tiny_cpu):
+    """Step graphs of another model or cache are refused before any launch."""
 
     class Foreign:
         model = None
@@ -322,3 +324,5 @@ def test_execute_model_batch_refuses_foreign_decode_graphs(tiny_cpu):
     model, cache = tiny_cpu
     with pytest.raises(ValueError, match="decode_graphs must belong to this model"):
         execute_model_batch(model, good_batch(), cache, decode_graphs=Foreign())
+    with pytest.raises(ValueError, match="prefill_graphs must belong to this model"):
+        execute_model_batch(model, good_batch(), cache, prefill_graphs=Foreign())
