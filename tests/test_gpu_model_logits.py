@@ -22,6 +22,9 @@ contiguous K/V, no paging):
   BF16_TOL, and the argmax equal wherever the oracle's top-2 margin exceeds
   BF16_MARGIN. The two sides round their bf16 GEMMs in different orders, and
   the differences compound over 24 layers; the logits reach about 3.2 here.
+- FP16 (the same, in fp16: the matrix-core prefill and one-launch decode
+  with fp16 operands): max-abs error at most FP16_TOL, the argmax equal
+  wherever the margin exceeds FP16_MARGIN.
 """
 
 from __future__ import annotations
@@ -47,6 +50,9 @@ pytestmark = pytest.mark.gpu
 # margin is twice the tolerance.
 FP32_TOL, FP32_MARGIN, FP32_MIN_CHECKS = 1e-5, 1e-4, 20
 BF16_TOL, BF16_MARGIN, BF16_MIN_CHECKS = 6.25e-2, 0.125, 8
+# FP16: four fp16 ulps of logits in [2, 4) (measured: at most 3.9e-3, about
+# two ulps); argmax checked wherever the margin is twice the tolerance.
+FP16_TOL, FP16_MARGIN, FP16_MIN_CHECKS = 7.8125e-3, 1.5625e-2, 12
 DECODE_STEPS = 5
 REQUESTS = ("init0", "init7", "init2", "arr0")  # prompts of 218, 687, 942, 1024 tokens
 
@@ -87,7 +93,8 @@ def run_teacher_forced(model, cfg, prompts, forced, dtype, device):
     return {rid: torch.stack(r) for rid, r in rows.items()}
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
+                         ids=["fp32", "bf16", "fp16"])
 def test_qwen05b_24_layer_teacher_forced_logits(device, serving_model, dtype):
     cfg, model, prompts = serving_model
     gen = torch.Generator().manual_seed(17)
@@ -96,9 +103,10 @@ def test_qwen05b_24_layer_teacher_forced_logits(device, serving_model, dtype):
     oracle = OracleQwen2(model.state_dict(), cfg, dtype=dtype)
     gpu_model = copy.deepcopy(model).to(device=device, dtype=dtype).eval()
     got = run_teacher_forced(gpu_model, cfg, prompts, forced, dtype, device)
-    tol, margin_bar, min_checks = ((FP32_TOL, FP32_MARGIN, FP32_MIN_CHECKS)
-                                   if dtype == torch.float32 else
-                                   (BF16_TOL, BF16_MARGIN, BF16_MIN_CHECKS))
+    tol, margin_bar, min_checks = {
+        torch.float32: (FP32_TOL, FP32_MARGIN, FP32_MIN_CHECKS),
+        torch.bfloat16: (BF16_TOL, BF16_MARGIN, BF16_MIN_CHECKS),
+        torch.float16: (FP16_TOL, FP16_MARGIN, FP16_MIN_CHECKS)}[dtype]
     worst, scale, checked = 0.0, 0.0, 0
     with torch.no_grad():
         for rid, prompt in prompts.items():
