@@ -164,10 +164,23 @@ class Qwen2DecoderLayer(nn.Module):
         self.post_attention_layernorm = Qwen2RMSNorm(config.hidden_size,
                                                      eps=config.rms_norm_eps)
 
+    def _block_parts(self, residual: torch.Tensor, delta: torch.Tensor | None, attend):
+        """The layer on the input residual + delta (delta None: the input is
+        residual), returned as (residual', delta') whose sum is the layer's
+        output. Each residual add rides in the launch of the norm after it
+        (Qwen2RMSNorm.forward_with_residual), with the bits of a separate add
+        followed by the norm."""
+        if delta is None:
+            normed = self.input_layernorm(residual)
+        else:
+            normed, residual = self.input_layernorm.forward_with_residual(delta, residual)
+        normed, residual = self.post_attention_layernorm.forward_with_residual(
+            attend(normed), residual)
+        return residual, self.mlp(normed)
+
     def _block(self, hidden_states: torch.Tensor, attend) -> torch.Tensor:
-        normed, hidden_states = self.post_attention_layernorm.forward_with_residual(
-            attend(self.input_layernorm(hidden_states)), hidden_states)
-        return hidden_states + self.mlp(normed)
+        residual, delta = self._block_parts(hidden_states, None, attend)
+        return residual + delta
 
     def forward(self, hidden_states: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
         return self._block(hidden_states, lambda h: self.self_attn(h, position_ids))
@@ -237,11 +250,18 @@ class TinyQwen2Model(nn.Module):
             raise ValueError("KV cache head_dim must match model head_dim "
                              f"({self.config.head_dim}), got {kv_cache.head_dim}")
 
-    def _run(self, input_ids: torch.Tensor, step) -> torch.Tensor:
-        hidden_states = self.embed_tokens(input_ids)
+    def _run(self, input_ids: torch.Tensor, attend_of) -> torch.Tensor:
+        """Embedding, the layers and the final norm; attend_of(layer, i) is
+        layer i's attention on its normed input. Between layers the hidden
+        state travels as (residual, delta), whose sum it is: the add of a
+        layer's MLP output rides in the next norm's launch, with the bits of a
+        separate add (Qwen2DecoderLayer._block_parts)."""
+        residual, delta = self.embed_tokens(input_ids), None
         for layer_idx, layer in enumerate(self.layers):
-            hidden_states = step(layer, layer_idx, hidden_states)
-        return self.norm(hidden_states)
+            residual, delta = layer._block_parts(residual, delta, attend_of(layer, layer_idx))
+        if delta is None:
+            return self.norm(residual)
+        return self.norm.forward_with_residual(delta, residual)[0]
 
     # Entry points -----------------------------------------------------------
     def forward(self, input_ids: torch.Tensor,
@@ -259,7 +279,7 @@ class TinyQwen2Model(nn.Module):
         elif position_ids.shape != input_ids.shape:
             raise ValueError("position_ids shape must match input_ids shape "
                              f"{tuple(input_ids.shape)}, got {tuple(position_ids.shape)}")
-        return self._run(input_ids, lambda layer, i, h: layer(h, position_ids))
+        return self._run(input_ids, lambda layer, i: lambda h: layer.self_attn(h, position_ids))
 
     def forward_prefill_with_cache(self, input_ids, position_ids, kv_cache,
                                    slot_mapping) -> torch.Tensor:
@@ -282,8 +302,10 @@ class TinyQwen2Model(nn.Module):
             raise ValueError("slot_mapping length must match sequence length "
                              f"({input_ids.shape[1]}), got {slot_mapping.shape[0]}")
         self._check_cache(kv_cache)
-        return self._run(input_ids, lambda layer, i, h: layer.forward_prefill_with_cache(
-            h, position_ids, kv_cache, i, slot_mapping))
+        return self._run(input_ids, lambda layer, i: lambda h:
+                         layer.self_attn.forward_prefill_with_cache(
+                             hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+                             layer_idx=i, slot_mapping=slot_mapping))
 
     def forward_decode_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
                                   block_table, context_len) -> torch.Tensor:
@@ -309,8 +331,11 @@ class TinyQwen2Model(nn.Module):
         if len(block_table) < -(-context_len // kv_cache.block_size):
             raise ValueError("block_table does not contain enough blocks for context_len")
         self._check_cache(kv_cache)
-        return self._run(input_ids, lambda layer, i, h: layer.forward_decode_with_cache(
-            h, position_ids, kv_cache, i, slot_mapping, block_table, context_len))
+        return self._run(input_ids, lambda layer, i: lambda h:
+                         layer.self_attn.forward_decode_with_cache(
+                             hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+                             layer_idx=i, slot_mapping=slot_mapping, block_table=block_table,
+                             context_len=context_len))
 
     def forward_decode_batch_with_cache(self, input_ids, position_ids, kv_cache, slot_mapping,
                                         block_tables, context_lens, *,
@@ -341,9 +366,12 @@ class TinyQwen2Model(nn.Module):
         # Every layer gets the same metadata tensors: the first layer checks
         # them (one host sync, before any cache write) and the others do not
         # repeat the checks.
-        return self._run(input_ids, lambda layer, i, h: layer.forward_decode_batch_with_cache(
-            h, position_ids, kv_cache, i, slot_mapping, block_tables, context_lens,
-            metadata_checked=metadata_checked or i > 0))
+        return self._run(input_ids, lambda layer, i: lambda h:
+                         layer.self_attn.forward_decode_batch_with_cache(
+                             hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+                             layer_idx=i, slot_mapping=slot_mapping, block_tables=block_tables,
+                             context_lens=context_lens,
+                             metadata_checked=metadata_checked or i > 0))
 
     def forward_prefill_packed_with_cache(self, input_ids: torch.Tensor,
                                           position_ids: torch.Tensor,
@@ -369,12 +397,12 @@ class TinyQwen2Model(nn.Module):
             self.check_prefill_packed_inputs(input_ids, position_ids, kv_cache, slot_mapping,
                                              block_tables, query_start_loc, context_lens,
                                              max_query_len)
-        hidden_states = self.embed_tokens(input_ids)
-        for layer_idx, layer in enumerate(self.layers):
-            hidden_states = layer.forward_prefill_packed_with_cache(
-                hidden_states, position_ids, kv_cache, layer_idx, slot_mapping, block_tables,
-                query_start_loc, context_lens, max_query_len)
-        return self.norm(hidden_states)
+        return self._run(input_ids, lambda layer, i: lambda h:
+                         layer.self_attn.forward_prefill_packed_with_cache(
+                             hidden_states=h, position_ids=position_ids, kv_cache=kv_cache,
+                             layer_idx=i, slot_mapping=slot_mapping, block_tables=block_tables,
+                             query_start_loc=query_start_loc, context_lens=context_lens,
+                             max_query_len=max_query_len))
 
     def check_prefill_packed_inputs(self, input_ids, position_ids, kv_cache, slot_mapping,
                                     block_tables, query_start_loc, context_lens,
