@@ -68,4 +68,10 @@ bool prefill_mfma_eligible(const PrefillParams &p, int dtype);
 int launch_prefill_mfma(const PrefillParams &p, int dtype, int64_t max_query_len,
                         hipStream_t stream);
 
+// True when the FP32 matrix-core kernel covers these arguments (FP32,
+// head_dim 64 or 128, power-of-two block_size >= 16, 16-byte aligned rows,
+// positive scale).
+bool prefill_f32_eligible(const PrefillParams &p, int dtype);
+int launch_prefill_f32(const PrefillParams &p, int64_t max_query_len, hipStream_t stream);
+
 }  // namespace mlr

@@ -159,6 +159,7 @@ int run_prefill(const PrefillParams &params, int dtype, int64_t max_qlen,
   p.bs_log2 = log2_if_pow2(p.block_size);
   if (prefill_mfma_eligible(p, dtype))
     return launch_prefill_mfma(p, dtype, max_qlen, stream);
+  if (prefill_f32_eligible(p, dtype)) return launch_prefill_f32(p, max_qlen, stream);
   switch (dtype) {
     case MLR_DTYPE_F32: return launch_generic<float>(p, max_qlen, stream);
     case MLR_DTYPE_F16: return launch_generic<f16_t>(p, max_qlen, stream);

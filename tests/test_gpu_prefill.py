@@ -63,7 +63,10 @@ CASES = [
     (torch.float16, 28, 4, 128, 16, 300, 200, 16),                 # fp16, D=128
     (torch.float16, 8, 8, 64, 32, 17, 100, 64),                    # fp16, G=1, BS=32
     (torch.float16, 14, 2, 64, 16, 1000, 77, 128),
-    (torch.float32, 14, 2, 64, 16, 250, 70, 64),
+    (torch.float32, 14, 2, 64, 16, 250, 70, 64),                   # FP32 matrix cores
+    (torch.float32, 28, 4, 128, 16, 300, 200, 16),                 # FP32, D=128
+    (torch.float32, 8, 8, 64, 32, 17, 100, 64),                    # FP32, G=1, BS=32
+    (torch.float32, 14, 2, 64, 16, 1000, 77, 128),
     (torch.float32, 6, 3, 40, 5, 11, 29, 7),
     (torch.float64, 4, 2, 16, 4, 9, 13, 4),
 ]
@@ -170,6 +173,21 @@ def test_fp16_tiling_edges_match_oracle(device, hq, hkv, d, bs, prefix, chunk):
     assert max_abs(got, want) <= 2e-2
 
 
+@pytest.mark.parametrize("hq,hkv,d,bs,prefix,chunk", EDGE_CASES,
+                         ids=[f"{c[0]}x{c[1]}-d{c[2]}-bs{c[3]}-p{c[4]}-c{c[5]}"
+                              for c in EDGE_CASES])
+def test_fp32_tiling_edges_match_oracle(device, hq, hkv, d, bs, prefix, chunk):
+    """The same tiling edges in FP32 (the FP32 matrix-core kernel: 16-query
+    waves, 64-query workgroups, 16-key blocks), within 1e-5."""
+    q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, torch.float32,
+                                 seed=prefix + chunk)
+    want = opa.prefill_chunk_tiled(q, kc, vc, table, prefix, prefix + chunk, bs, 64)
+    got = kpa.paged_attention_prefill_chunk_tiled(
+        q.to(device), kc.to(device), vc.to(device), table, prefix, prefix + chunk, bs, 64)
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) <= 1e-5
+
+
 def test_bf16_ragged_varlen_matches_oracle(device):
     """One launch over sequences of 1..300 queries with unrelated prefixes."""
     hq, hkv, d, bs = 14, 2, 64, 16
@@ -247,12 +265,13 @@ def test_bf16_many_sequences_match_oracle(device, num_seqs):
         assert max_abs(got[lo:hi], want) <= 2e-2, f"sequence {s}"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("d,bs", [(64, 16), (128, 32), (40, 5)], ids=["d64", "d128", "generic"])
-def test_out_of_range_block_masks_its_tokens(device, d, bs):
+def test_out_of_range_block_masks_its_tokens(device, d, bs, dtype):
     """An out-of-range block id in the table hides that block's keys."""
     from oracle import textbook
     hq, hkv, prefix, chunk = 4, 2, 70, 40
-    q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, torch.bfloat16, seed=5)
+    q, kc, vc, table = make_case(hq, hkv, prefix, chunk, d, bs, dtype, seed=5)
     bad_blk = 1  # a prefix block: its keys are visible to every query
     context = prefix + chunk
     visible = [[j <= prefix + i and j // bs != bad_blk for j in range(context)]
@@ -270,4 +289,4 @@ def test_out_of_range_block_masks_its_tokens(device, d, bs):
         torch.tensor([0, chunk], dtype=torch.long).to(device),
         torch.tensor([context], dtype=torch.long).to(device), chunk).cpu()
     assert torch.isfinite(got).all()
-    assert max_abs(got, want) <= 2e-2
+    assert max_abs(got, want) <= TOL[dtype]
