@@ -81,6 +81,7 @@ METRIC = ("paged decode attn GB/s (% of HBM peak); "
           "chunk-prefill attn TFLOP/s (% MFMA)")
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 LAYERS = 24
 
 
@@ -1478,6 +1479,13 @@ def main():
             "us_per_call": pre16["us_per_call"],
             "tflops": round(pre16["tflops"], 3),
             "frac_of_fp16_peak": round(pre16["tflops"] / BF16_PEAK_TFLOPS, 5)}
+        pre32 = bench_prefill(device, dtype=torch.float32)
+        line["prefill"]["fp32"] = {
+            "what": ("the same call in FP32 (v_mfma_f32_16x16x4_f32), against the 157.3 "
+                     "TFLOP/s FP32 matrix-core peak"),
+            "us_per_call": pre32["us_per_call"],
+            "tflops": round(pre32["tflops"], 3),
+            "frac_of_fp32_peak": round(pre32["tflops"] / F32_PEAK_TFLOPS, 5)}
     line["fp32_decode_b4"] = bench_fp32_decode_b4(
         device, 0 if args.no_cpu_baseline else args.cpu_budget / 4)
     if not args.no_pre_attention:
