@@ -596,7 +596,10 @@ def bench_pre_attention(device, reps=4, calls_per_graph=100):
     ahead of the GPU (with 10-call graphs they do not, and the per-call time
     grows by ~2 us). `graph_node_us` is the same measurement for a one-element
     fill kernel: the per-launch cost a graph node adds, which the `_net`
-    figures subtract."""
+    figures subtract. `same_bytes_elementwise_us` times a PyTorch elementwise
+    kernel that reads the projection output and writes a tensor of its size
+    (torch.mul(qkv, 1, out=...)): about the bytes the fused kernel moves, with
+    no rotation, scatter or position loads, as a comparator."""
     import types
 
     import torch
@@ -648,6 +651,8 @@ def bench_pre_attention(device, reps=4, calls_per_graph=100):
             cache.write_slots(slots, k[0], v[0], 0, validate=False)
 
         k_us = graph_us(kernel)
+        dst = torch.empty_like(qkv)
+        copy_us = graph_us(lambda: torch.mul(qkv, 1, out=dst))
         out[str(tokens)] = {
             "fused_kernel_us": round(k_us, 3),
             "fused_kernel_net_us": round(k_us - node_us, 3),
@@ -656,6 +661,8 @@ def bench_pre_attention(device, reps=4, calls_per_graph=100):
             "kernel_bytes": tokens * bytes_per_token,
             "kernel_GBps": round(tokens * bytes_per_token / k_us / 1e3, 1),
             "kernel_net_GBps": round(tokens * bytes_per_token / (k_us - node_us) / 1e3, 1),
+            "same_bytes_elementwise_us": round(copy_us, 3),
+            "same_bytes_elementwise_bytes": 2 * qkv.numel() * qkv.element_size(),
         }
     big = out["2048"]
     return {
