@@ -12,8 +12,13 @@ the step goes through one packed forward (``forward_prefill_packed_with_cache``:
 one varlen prefill launch per layer), and the decodes through one batched
 decode forward, as in the reference. Logits come back in packed token order
 whatever the order of phases in the batch. The batch checks are the
-reference's, with its messages and order, evaluated with two host syncs
-instead of several per request.
+reference's, with its messages and order, evaluated with one host sync
+instead of several per request. Every check that reads the device (the
+batch's, then the packed prefill's and the batched decode's metadata) runs
+before either forward is queued, and the index lists reach the device through
+pinned memory without a wait: once a forward is queued, a host sync or a
+pageable upload would stall the host until its kernels finish, and the GPU
+would then idle while the host prepares the next forward.
 
 With ``decode_graphs`` (runtime/step_graphs.py) the decodes of a step
 replay a HIP graph of the batched decode forward, recorded once per batch
@@ -32,6 +37,7 @@ from dataclasses import dataclass
 import torch
 
 from ..kernels import paged_attention as kpa
+from ..model.qwen2_attention import Qwen2Attention
 from .paged_kv_cache import PagedKVCache
 from .request import Request, RequestStatus
 from .scheduler import Scheduler, SchedulerOutput
@@ -195,6 +201,17 @@ def _build_on_device(entries, block_size: int, dev: torch.device) -> ModelBatch:
     )
 
 
+def _upload(values, device: torch.device) -> torch.Tensor:
+    """A host list of ints as an int64 tensor on `device`. For a GPU the list
+    is staged in pinned memory and copied asynchronously on the current
+    stream, so the host does not wait for the kernels already queued there
+    (a copy from pageable memory would)."""
+    if device.type != "cuda":
+        return torch.tensor(values, dtype=torch.long, device=device)
+    staged = torch.tensor(values, dtype=torch.long, pin_memory=True)
+    return staged.to(device, non_blocking=True)
+
+
 def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list[int], int]:
     """The reference's execute_model_batch checks (:154-243), in its order.
     Returns the host copy of query_start_loc and the packed token count."""
@@ -241,22 +258,25 @@ def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list
     if batch.query_start_loc.numel() != n + 1:
         raise ValueError("query_start_loc must contain one more entry than request_ids")
 
-    # Everything the data-dependent checks need, in one transfer.
-    qsl = batch.query_start_loc.tolist()
-    ctx = batch.context_lens.tolist()
+    # Everything the data-dependent checks need, in one transfer: the query
+    # offsets, the context lengths and, per request, whether a block its
+    # context uses lies outside the cache (blocks needed: ceil(ctx / bs), none
+    # for ctx <= 0).
+    bs, width = kv_cache.block_size, batch.block_tables.shape[1]
+    required_dev = torch.div(batch.context_lens + (bs - 1), bs,
+                             rounding_mode="floor").clamp_(min=0)
+    used = torch.arange(width, device=device)[None, :] < required_dev[:, None]
+    bad = (used & ((batch.block_tables < 0)
+                   | (batch.block_tables >= kv_cache.num_blocks))).any(dim=1)
+    host = torch.cat([batch.query_start_loc, batch.context_lens, bad.long()]).tolist()
+    qsl, ctx, bad_rows = host[:n + 1], host[n + 1:2 * n + 1], host[2 * n + 1:]
     if qsl[0] != 0:
         raise ValueError("query_start_loc must start at 0")
     if any(b <= a for a, b in zip(qsl, qsl[1:])):
         raise ValueError("query_start_loc must be strictly increasing")
     if qsl[-1] != num_tokens:
         raise ValueError("query_start_loc must end at the packed token count")
-    bs, width = kv_cache.block_size, batch.block_tables.shape[1]
     required = [-(-c // bs) if c > 0 else 0 for c in ctx]
-    cols = torch.arange(width, device=device)
-    req_t = torch.tensor(required, dtype=torch.long, device=device)
-    used = cols[None, :] < req_t[:, None]
-    bad_rows = (used & ((batch.block_tables < 0)
-                        | (batch.block_tables >= kv_cache.num_blocks))).any(dim=1).tolist()
     for i, request_id in enumerate(batch.request_ids):
         if ctx[i] <= 0:
             raise ValueError(f"Request {request_id} context_len must be greater than 0")
@@ -292,6 +312,7 @@ def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
     prefill = [i for i, ph in enumerate(batch.request_phases) if ph is RequestStatus.PREFILLING]
     decode = [i for i, ph in enumerate(batch.request_phases) if ph is RequestStatus.DECODING]
 
+    packed = step = None
     if prefill:
         lens = [qsl[i + 1] - qsl[i] for i in prefill]
         contiguous = prefill == list(range(len(prefill)))
@@ -299,39 +320,50 @@ def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
             rows = slice(0, qsl[len(prefill)])
             pick = lambda t: t[rows]  # noqa: E731
         else:
-            idx = torch.cat([torch.arange(qsl[i], qsl[i + 1]) for i in prefill]).to(device)
+            idx = _upload([t for i in prefill for t in range(qsl[i], qsl[i + 1])], device)
             pick = lambda t: t.index_select(0, idx)  # noqa: E731
-        req = torch.tensor(prefill, dtype=torch.long, device=device)
+        req = _upload(prefill, device)
         offsets = [0]
         for n in lens:
             offsets.append(offsets[-1] + n)
         packed = (pick(batch.input_token_ids), pick(batch.positions), pick(batch.slot_mapping),
-                  batch.block_tables.index_select(0, req),
-                  torch.tensor(offsets, dtype=torch.long, device=device),
+                  batch.block_tables.index_select(0, req), _upload(offsets, device),
                   batch.context_lens.index_select(0, req))
+    if decode:
+        req = _upload(decode, device)
+        decode_rows = _upload([qsl[i] for i in decode], device)
+        step = dict(input_ids=batch.input_token_ids.index_select(0, decode_rows).unsqueeze(1),
+                    position_ids=batch.positions.index_select(0, decode_rows).unsqueeze(1),
+                    slot_mapping=batch.slot_mapping.index_select(0, decode_rows),
+                    block_tables=batch.block_tables.index_select(0, req),
+                    context_lens=batch.context_lens.index_select(0, req))
+
+    # The metadata checks of both forwards (one host sync each) before either
+    # is queued; the forwards then skip them.
+    if packed is not None:
+        model.model.check_prefill_packed_inputs(*packed[:2], kv_cache, *packed[2:], max(lens))
+    if step is not None:
+        Qwen2Attention._check_decode_metadata(kv_cache, step["position_ids"],
+                                              step["slot_mapping"], step["block_tables"],
+                                              step["context_lens"])
+
+    if packed is not None:
         if prefill_graphs is not None:
-            out = prefill_graphs(*packed, max(lens))
+            out = prefill_graphs(*packed, max(lens), metadata_checked=True)
         else:
             out = model.forward_prefill_packed_with_cache(*packed[:2], kv_cache, *packed[2:],
-                                                          max(lens))
+                                                          max(lens), metadata_checked=True)
         if contiguous:
             logits[rows] = out
         else:
             logits.index_copy_(0, idx, out)
-
-    if decode:
-        req = torch.tensor(decode, dtype=torch.long, device=device)
-        rows = torch.tensor([qsl[i] for i in decode], dtype=torch.long, device=device)
-        step = dict(input_ids=batch.input_token_ids.index_select(0, rows).unsqueeze(1),
-                    position_ids=batch.positions.index_select(0, rows).unsqueeze(1),
-                    slot_mapping=batch.slot_mapping.index_select(0, rows),
-                    block_tables=batch.block_tables.index_select(0, req),
-                    context_lens=batch.context_lens.index_select(0, req))
+    if step is not None:
         if decode_graphs is not None:
-            out = decode_graphs(**step)
+            out = decode_graphs(**step, metadata_checked=True)
         else:
-            out = model.forward_decode_batch_with_cache(kv_cache=kv_cache, **step)
-        logits.index_copy_(0, rows, out.squeeze(1))
+            out = model.forward_decode_batch_with_cache(kv_cache=kv_cache, **step,
+                                                        metadata_checked=True)
+        logits.index_copy_(0, decode_rows, out.squeeze(1))
     return logits
 
 
@@ -343,16 +375,24 @@ def greedy_sample(packed_logits: torch.Tensor, batch: ModelBatch) -> dict[str, i
         raise ValueError("packed_logits token dimension must match ModelBatch tokens")
     if len(batch.request_ids) + 1 != batch.query_start_loc.numel():
         raise ValueError("query_start_loc must contain one more entry than request_ids")
-    qsl = batch.query_start_loc.tolist()
+    n = len(batch.request_ids)
+    if n and packed_logits.shape[0]:
+        # Each request's last row on the device, clamped so that the gather
+        # stays in bounds whatever query_start_loc holds: the offsets and the
+        # picks come back in one transfer, and the offsets are checked below.
+        qsl_dev = batch.query_start_loc
+        last = (qsl_dev[1:] - 1).clamp(0, packed_logits.shape[0] - 1)
+        picks_dev = packed_logits.index_select(0, last).argmax(dim=-1)
+        host = torch.cat([qsl_dev, picks_dev.to(qsl_dev.device)]).tolist()
+        qsl, picks = host[:n + 1], host[n + 1:]
+    else:
+        qsl, picks = batch.query_start_loc.tolist(), []
     for i, request_id in enumerate(batch.request_ids):
         if qsl[i + 1] <= qsl[i]:
             raise ValueError(f"Request {request_id} must contain at least one query token")
     if not batch.request_ids:
         return {}
-    last = torch.tensor([end - 1 for end in qsl[1:]], dtype=torch.long,
-                        device=packed_logits.device)
-    picks = packed_logits.index_select(0, last).argmax(dim=-1).tolist()
-    return dict(zip(batch.request_ids, (int(t) for t in picks)))
+    return dict(zip(batch.request_ids, picks))
 
 
 def run_generation_step(model, scheduler: Scheduler,

@@ -227,17 +227,22 @@ class DecodeGraphs:
 
     def __call__(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
                  slot_mapping: torch.Tensor, block_tables: torch.Tensor,
-                 context_lens: torch.Tensor) -> torch.Tensor:
+                 context_lens: torch.Tensor, *, metadata_checked: bool = False) -> torch.Tensor:
         """[B, 1] token ids -> [B, 1, vocab_size] logits (the graph's output
-        buffer, valid until the next call with this batch size)."""
+        buffer, valid until the next call with this batch size).
+
+        metadata_checked: the caller already ran the device-side metadata
+        checks (Qwen2Attention._check_decode_metadata) on these tensors
+        against this cache, so the call makes no host sync."""
         batch = self._check(input_ids, position_ids, slot_mapping, block_tables, context_lens)
         if block_tables.shape[1] > self.width:
             self.eager_calls += 1
             return self.model.forward_decode_batch_with_cache(
                 input_ids, position_ids, self.kv_cache, slot_mapping, block_tables,
-                context_lens)
-        Qwen2Attention._check_decode_metadata(self.kv_cache, position_ids, slot_mapping,
-                                              block_tables, context_lens)
+                context_lens, metadata_checked=metadata_checked)
+        if not metadata_checked:
+            Qwen2Attention._check_decode_metadata(self.kv_cache, position_ids, slot_mapping,
+                                                  block_tables, context_lens)
         r = self._recorded.get(batch)
         if r is None:
             r = _Recorded(batch, self.width, self.device)
@@ -312,12 +317,17 @@ class PrefillGraphs:
     def __call__(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
                  slot_mapping: torch.Tensor, block_tables: torch.Tensor,
                  query_start_loc: torch.Tensor, context_lens: torch.Tensor,
-                 max_query_len: int) -> torch.Tensor:
+                 max_query_len: int, *, metadata_checked: bool = False) -> torch.Tensor:
         """[T] token ids -> [T, vocab_size] logits (for a replay, the graph's
-        output buffer, valid until that shape's next replay)."""
-        self.model.model.check_prefill_packed_inputs(
-            input_ids, position_ids, self.kv_cache, slot_mapping, block_tables,
-            query_start_loc, context_lens, max_query_len)
+        output buffer, valid until that shape's next replay).
+
+        metadata_checked: the caller already ran the model's
+        check_prefill_packed_inputs on these tensors against this cache, so
+        the call makes no host sync."""
+        if not metadata_checked:
+            self.model.model.check_prefill_packed_inputs(
+                input_ids, position_ids, self.kv_cache, slot_mapping, block_tables,
+                query_start_loc, context_lens, max_query_len)
         key = (input_ids.shape[0], context_lens.shape[0], int(max_query_len),
                block_tables.shape[1])
         args = (input_ids, position_ids, slot_mapping, block_tables, query_start_loc,
