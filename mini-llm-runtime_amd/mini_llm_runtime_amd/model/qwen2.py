@@ -497,6 +497,25 @@ class TinyQwen2ForCausalLM(nn.Module):
     def forward(self, input_ids, position_ids=None) -> torch.Tensor:
         return self.lm_head(self.model(input_ids, position_ids))
 
+    def logits(self, hidden_states: torch.Tensor, out: torch.Tensor | None = None
+               ) -> torch.Tensor:
+        """lm_head(hidden_states) for [N, hidden_size] rows. With `out`
+        (a contiguous [N, vocab_size] tensor, e.g. a row range of a larger
+        logits buffer) the GEMM writes its result there directly instead of
+        into a new tensor that the caller would then copy: the same product
+        as the module's forward (lm_head has no bias). The GEMM library may
+        pick its kernel by the operands' address alignment, so `out` is
+        written directly only when it is 256-byte aligned like a new
+        allocation; otherwise the product goes to a new tensor and is copied."""
+        if out is None:
+            return self.lm_head(hidden_states)
+        if (out.shape != (hidden_states.shape[0], self.lm_head.out_features)
+                or not out.is_contiguous()):
+            raise ValueError("out must be a contiguous [N, vocab_size] tensor")
+        if out.data_ptr() % 256:
+            return out.copy_(self.lm_head(hidden_states))
+        return torch.mm(hidden_states, self.lm_head.weight.t(), out=out)
+
     def forward_prefill_with_cache(self, input_ids, position_ids, kv_cache,
                                    slot_mapping) -> torch.Tensor:
         return self.lm_head(self.model.forward_prefill_with_cache(

@@ -347,23 +347,29 @@ def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
                                               step["slot_mapping"], step["block_tables"],
                                               step["context_lens"])
 
+    # Each forward's LM head writes its rows of `logits` directly where they
+    # are contiguous (the prefills lead in build_model_batch's order and the
+    # decodes follow), instead of into a new tensor copied in afterwards.
     if packed is not None:
+        target = logits[rows] if contiguous else None
         if prefill_graphs is not None:
-            out = prefill_graphs(*packed, max(lens), metadata_checked=True)
+            out = prefill_graphs(*packed, max(lens), metadata_checked=True, out=target)
         else:
-            out = model.forward_prefill_packed_with_cache(*packed[:2], kv_cache, *packed[2:],
-                                                          max(lens), metadata_checked=True)
-        if contiguous:
-            logits[rows] = out
-        else:
+            out = model.logits(model.model.forward_prefill_packed_with_cache(
+                *packed[:2], kv_cache, *packed[2:], max(lens), metadata_checked=True), target)
+        if not contiguous:
             logits.index_copy_(0, idx, out)
     if step is not None:
+        target = None
+        if decode[-1] - decode[0] == len(decode) - 1:  # consecutive one-token requests
+            target = logits[qsl[decode[0]]:qsl[decode[0]] + len(decode)]
         if decode_graphs is not None:
-            out = decode_graphs(**step, metadata_checked=True)
+            out = decode_graphs(**step, metadata_checked=True, out=target)
         else:
-            out = model.forward_decode_batch_with_cache(kv_cache=kv_cache, **step,
-                                                        metadata_checked=True)
-        logits.index_copy_(0, decode_rows, out.squeeze(1))
+            out = model.logits(model.model.forward_decode_batch_with_cache(
+                kv_cache=kv_cache, **step, metadata_checked=True)[:, 0], target)
+        if target is None:
+            logits.index_copy_(0, decode_rows, out.reshape(len(decode), -1))
     return logits
 
 

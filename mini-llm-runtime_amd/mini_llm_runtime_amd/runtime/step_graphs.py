@@ -38,8 +38,10 @@ batch size puts row j at position j % block_size of a block the runner holds
 nothing outside those blocks. The blocks come from the cache's allocator, as
 a sequence of the runner's own, and go back with ``release()``.
 
-The returned logits are the graph's static output, valid until the next call
-with the same batch size. Graphs hold the weights and the cache as they were
+A graph ends at the final norm's hidden states: the LM head runs after the
+replay, into ``out`` when the caller passes one (the runner passes the decode
+rows of its packed logits, so they are written once and not copied) and into
+a new tensor otherwise. Graphs hold the weights and the cache as they were
 recorded: replace a weight or the cache and call ``reset()``. Replays must not
 overlap (one stream at a time): the graphs of one runner share its decode
 workspace. A block table wider than ``max_blocks_per_seq`` runs the same step
@@ -53,7 +55,9 @@ longest query and block-table width (the prefill launch's grid follows from
 them; the offsets, lengths, slots and tables are read on the device). A shape
 runs eagerly until it is met for the ``record_at``-th time, and is recorded
 then; at most ``max_graphs`` recordings are kept (least recently used
-dropped), as each holds its logits buffer ([tokens, vocab]). Only a runner's
+dropped), as each holds its static buffers (the hidden states, [tokens,
+hidden], and the forward's intermediates in its private pool). As for the
+decode, the LM head runs after the replay, into ``out`` when given. Only a runner's
 first recording runs the eager step before its capture: the packed prefill
 uses no decode workspace, and the model's cached weights and the stream's
 GEMM state exist from then on. Every call runs the model's
@@ -81,7 +85,7 @@ class _Recorded:
         self.block_tables = torch.full((batch, width), -1, dtype=torch.long, device=device)
         self.context_lens = torch.ones(batch, dtype=torch.long, device=device)
         self.graph: torch.cuda.CUDAGraph | None = None
-        self.logits: torch.Tensor | None = None
+        self.hidden: torch.Tensor | None = None
 
     def load(self, input_ids, position_ids, slot_mapping, block_tables, context_lens) -> None:
         width = block_tables.shape[1]
@@ -217,19 +221,26 @@ class DecodeGraphs:
         return batch
 
     def _step(self, r: _Recorded) -> torch.Tensor:
-        return self.model.forward_decode_batch_with_cache(
+        return self.model.model.forward_decode_batch_with_cache(
             r.input_ids, r.position_ids, self.kv_cache, r.slot_mapping, r.block_tables,
             r.context_lens, metadata_checked=True)
 
     def _record(self, r: _Recorded) -> None:
-        r.graph, r.logits = _record(self.device, self.stream, lambda: self._step(r))
+        r.graph, r.hidden = _record(self.device, self.stream, lambda: self._step(r))
         self.captures += 1
+
+    def _logits(self, hidden: torch.Tensor, out: torch.Tensor | None) -> torch.Tensor:
+        if out is None:
+            return self.model.logits(hidden)
+        return self.model.logits(hidden[:, 0], out)
 
     def __call__(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
                  slot_mapping: torch.Tensor, block_tables: torch.Tensor,
-                 context_lens: torch.Tensor, *, metadata_checked: bool = False) -> torch.Tensor:
-        """[B, 1] token ids -> [B, 1, vocab_size] logits (the graph's output
-        buffer, valid until the next call with this batch size).
+                 context_lens: torch.Tensor, *, metadata_checked: bool = False,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """[B, 1] token ids -> [B, 1, vocab_size] logits, or the logits
+        written into `out` (a contiguous [B, vocab_size] tensor) and `out`
+        returned.
 
         metadata_checked: the caller already ran the device-side metadata
         checks (Qwen2Attention._check_decode_metadata) on these tensors
@@ -237,9 +248,9 @@ class DecodeGraphs:
         batch = self._check(input_ids, position_ids, slot_mapping, block_tables, context_lens)
         if block_tables.shape[1] > self.width:
             self.eager_calls += 1
-            return self.model.forward_decode_batch_with_cache(
+            return self._logits(self.model.model.forward_decode_batch_with_cache(
                 input_ids, position_ids, self.kv_cache, slot_mapping, block_tables,
-                context_lens, metadata_checked=metadata_checked)
+                context_lens, metadata_checked=metadata_checked), out)
         if not metadata_checked:
             Qwen2Attention._check_decode_metadata(self.kv_cache, position_ids, slot_mapping,
                                                   block_tables, context_lens)
@@ -253,7 +264,7 @@ class DecodeGraphs:
             r.load(input_ids, position_ids, slot_mapping, block_tables, context_lens)
         r.graph.replay()
         self.replays += 1
-        return r.logits
+        return self._logits(r.hidden, out)
 
 
 class _PrefillRecorded:
@@ -270,7 +281,7 @@ class _PrefillRecorded:
         self.query_start_loc = zeros(requests + 1)
         self.context_lens = zeros(requests)
         self.graph: torch.cuda.CUDAGraph | None = None
-        self.logits: torch.Tensor | None = None
+        self.hidden: torch.Tensor | None = None
 
     def load(self, input_ids, position_ids, slot_mapping, block_tables, query_start_loc,
              context_lens) -> None:
@@ -317,9 +328,10 @@ class PrefillGraphs:
     def __call__(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
                  slot_mapping: torch.Tensor, block_tables: torch.Tensor,
                  query_start_loc: torch.Tensor, context_lens: torch.Tensor,
-                 max_query_len: int, *, metadata_checked: bool = False) -> torch.Tensor:
-        """[T] token ids -> [T, vocab_size] logits (for a replay, the graph's
-        output buffer, valid until that shape's next replay).
+                 max_query_len: int, *, metadata_checked: bool = False,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """[T] token ids -> [T, vocab_size] logits, or the logits written
+        into `out` (a contiguous [T, vocab_size] tensor) and `out` returned.
 
         metadata_checked: the caller already ran the model's
         check_prefill_packed_inputs on these tensors against this cache, so
@@ -340,12 +352,13 @@ class PrefillGraphs:
             self._seen[key] = seen
             if seen < self.record_at:
                 self.eager_calls += 1
-                return self.model.forward_prefill_packed_with_cache(
-                    *args[:2], self.kv_cache, *args[2:], max_query_len, metadata_checked=True)
+                return self.model.logits(self.model.model.forward_prefill_packed_with_cache(
+                    *args[:2], self.kv_cache, *args[2:], max_query_len, metadata_checked=True),
+                    out)
             r = _PrefillRecorded(key[0], key[1], key[3], self.device)
             r.load(*args)
-            r.graph, r.logits = _record(self.device, self.stream, lambda: (
-                self.model.forward_prefill_packed_with_cache(
+            r.graph, r.hidden = _record(self.device, self.stream, lambda: (
+                self.model.model.forward_prefill_packed_with_cache(
                     r.input_ids, r.position_ids, self.kv_cache, r.slot_mapping,
                     r.block_tables, r.query_start_loc, r.context_lens, key[2],
                     metadata_checked=True)), warm=not self._warmed)
@@ -359,4 +372,4 @@ class PrefillGraphs:
             r.load(*args)
         r.graph.replay()
         self.replays += 1
-        return r.logits
+        return self.model.logits(r.hidden, out)

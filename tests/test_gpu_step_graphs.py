@@ -264,6 +264,51 @@ def test_prefill_replays_equal_the_eager_forward(device, dtype, prefixes):
     assert (graphs.eager_calls, graphs.captures, graphs.replays) == (1, 1, 3)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_logits_written_into_out_rows(device, dtype):
+    """With out= (a row range of a larger buffer, as the runner passes its
+    packed logits) both graph kinds and model.logits write exactly the logits
+    they return without it: at a 256-byte-aligned row offset (written by the
+    GEMM in place) and at an unaligned one (computed, then copied); the rows
+    around the range stay untouched."""
+    model = _model(device, dtype)
+    cache_g, cache_e = _cache(device, dtype), _cache(device, dtype)
+    dgraphs = DecodeGraphs(model, cache_g, max_blocks_per_seq=WIDTH)
+    pgraphs = PrefillGraphs(model, cache_g, record_at=1)
+    vocab = QWEN_2L["vocab_size"]
+    row_bytes = vocab * torch.tensor([], dtype=dtype).element_size()
+    aligned = next(r for r in range(1, 257) if (r * row_bytes) % 256 == 0)
+    gen = torch.Generator().manual_seed(24)
+    with torch.no_grad():
+        for offset in (aligned, 3):
+            step = _step(device, [5, 300, 17], gen)
+            want = model.forward_decode_batch_with_cache(kv_cache=cache_e,
+                                                         **_padded(step, WIDTH))[:, 0]
+            buf = torch.full((offset + 3 + 2, vocab), 7.0, dtype=dtype, device=device)
+            got = dgraphs(**step, out=buf[offset:offset + 3])
+            assert got.data_ptr() == buf[offset].data_ptr()
+            assert torch.equal(buf[offset:offset + 3], want), f"decode, offset {offset}"
+            assert (buf[:offset] == 7).all() and (buf[offset + 3:] == 7).all()
+
+            pstep, max_q = _prefill_step(device, [40, 21], [0, 0], gen)
+            want = model.forward_prefill_packed_with_cache(
+                pstep["input_ids"], pstep["position_ids"], cache_e, pstep["slot_mapping"],
+                pstep["block_tables"], pstep["query_start_loc"], pstep["context_lens"], max_q)
+            buf = torch.full((offset + 61 + 2, vocab), 7.0, dtype=dtype, device=device)
+            pgraphs(**pstep, max_query_len=max_q, out=buf[offset:offset + 61])
+            assert torch.equal(buf[offset:offset + 61], want), f"prefill, offset {offset}"
+            assert (buf[:offset] == 7).all() and (buf[offset + 61:] == 7).all()
+            assert torch.equal(cache_g.k_cache, cache_e.k_cache)
+            assert torch.equal(cache_g.v_cache, cache_e.v_cache)
+
+            hidden = torch.randn(9, QWEN_2L["hidden_size"], device=device).to(dtype)
+            buf = torch.zeros(offset + 9, vocab, dtype=dtype, device=device)
+            model.logits(hidden, buf[offset:])
+            assert torch.equal(buf[offset:], model.lm_head(hidden))
+    with pytest.raises(ValueError, match="contiguous"):
+        model.logits(hidden, buf[:, :vocab - 1])
+
+
 def test_prefill_graphs_keep_the_most_recent_shapes(device):
     """With max_graphs=1 two alternating shapes keep replacing each other's
     recording; results stay equal to the eager forward."""
