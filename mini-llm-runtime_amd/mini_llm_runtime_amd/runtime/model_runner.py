@@ -13,12 +13,14 @@ one varlen prefill launch per layer), and the decodes through one batched
 decode forward, as in the reference. Logits come back in packed token order
 whatever the order of phases in the batch. The batch checks are the
 reference's, with its messages and order, evaluated with one host sync
-instead of several per request. Every check that reads the device (the
-batch's, then the packed prefill's and the batched decode's metadata) runs
-before either forward is queued, and the index lists reach the device through
-pinned memory without a wait: once a forward is queued, a host sync or a
-pageable upload would stall the host until its kernels finish, and the GPU
-would then idle while the host prepares the next forward.
+instead of several per request; the same pass also runs the checks the
+packed prefill forward and the batched decode forward would otherwise make
+on their parts of the batch (positions, slots and distinct slots per phase,
+with those forwards' messages), so both run with ``metadata_checked``. The
+index lists reach the device through pinned memory without a wait: once a
+forward is queued, a host sync or a pageable upload would stall the host until
+its kernels finish, and the GPU would then idle while the host prepares the
+next forward.
 
 With ``decode_graphs`` (runtime/step_graphs.py) the decodes of a step
 replay a HIP graph of the batched decode forward, recorded once per batch
@@ -37,7 +39,6 @@ from dataclasses import dataclass
 import torch
 
 from ..kernels import paged_attention as kpa
-from ..model.qwen2_attention import Qwen2Attention
 from .paged_kv_cache import PagedKVCache
 from .request import Request, RequestStatus
 from .scheduler import Scheduler, SchedulerOutput
@@ -213,8 +214,19 @@ def _upload(values, device: torch.device) -> torch.Tensor:
 
 
 def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list[int], int]:
-    """The reference's execute_model_batch checks (:154-243), in its order.
-    Returns the host copy of query_start_loc and the packed token count."""
+    """The reference's execute_model_batch checks (:154-243), in its order,
+    then the metadata checks of the two forwards that execute_model_batch runs
+    on parts of the batch: the packed prefill's
+    (TinyQwen2Model.check_prefill_packed_inputs) on the prefilling requests,
+    then the batched decode's (Qwen2Attention._check_decode_metadata) on the
+    decoding ones, with their messages and order; all of it with one host
+    sync. Of those forwards' checks, the ones on query_start_loc, max_query_len
+    and the block tables hold by construction or by the checks above; the rest
+    are evaluated here over the whole batch: each token's position (prefill:
+    context_len - num_tokens + its offset; decode: context_len - 1, the same
+    formula for one token), its slot against the block table, and distinct
+    slots among the prefill tokens and among the decode tokens. Returns the
+    host copy of query_start_loc and the packed token count."""
     n = len(batch.request_ids)
     if len(batch.request_phases) != n:
         raise ValueError("request_phases length must match request_ids")
@@ -268,8 +280,11 @@ def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list
     used = torch.arange(width, device=device)[None, :] < required_dev[:, None]
     bad = (used & ((batch.block_tables < 0)
                    | (batch.block_tables >= kv_cache.num_blocks))).any(dim=1)
-    host = torch.cat([batch.query_start_loc, batch.context_lens, bad.long()]).tolist()
-    qsl, ctx, bad_rows = host[:n + 1], host[n + 1:2 * n + 1], host[2 * n + 1:]
+    flags = _step_metadata_flags(batch, bs, width, device)
+    host = torch.cat([batch.query_start_loc, batch.context_lens, bad.long(),
+                      flags.long()]).tolist()
+    qsl, ctx, bad_rows = host[:n + 1], host[n + 1:2 * n + 1], host[2 * n + 1:3 * n + 1]
+    flags = host[3 * n + 1:]
     if qsl[0] != 0:
         raise ValueError("query_start_loc must start at 0")
     if any(b <= a for a, b in zip(qsl, qsl[1:])):
@@ -292,7 +307,59 @@ def _check_batch(model, batch: ModelBatch, kv_cache: PagedKVCache) -> tuple[list
         elif phase is not RequestStatus.PREFILLING:
             raise ValueError(f"Unsupported request phase {phase} for request "
                              f"{batch.request_ids[i]}")
+    prefilling = [i for i, ph in enumerate(batch.request_phases)
+                  if ph is RequestStatus.PREFILLING]
+    if prefilling:
+        if any(ctx[i] < qsl[i + 1] - qsl[i] for i in prefilling):
+            raise ValueError("context_lens must cover each request's tokens")
+        if flags[0]:
+            raise ValueError("position_ids must run from context_len - num_tokens "
+                             "to context_len - 1 for each request")
+        if flags[1]:
+            raise ValueError("slot_mapping must match block_tables and positions")
+        if flags[2]:
+            raise ValueError("packed tokens must use distinct write slots")
+    if flags[3]:
+        raise ValueError("decode positions must equal context_lens - 1")
+    if flags[4]:
+        raise ValueError("slot_mapping must match block_tables and positions")
+    if flags[5]:
+        raise ValueError("decode requests must use distinct write slots")
     return qsl, num_tokens
+
+
+def _step_metadata_flags(batch: ModelBatch, bs: int, width: int,
+                         device: torch.device) -> torch.Tensor:
+    """Six device flags over the packed tokens: (prefill tokens) a position
+    that is not context_len - num_tokens + offset, a slot that does not match
+    the block table, a repeated slot; the same three for the decode tokens.
+    Every index is clamped into range, so the gathers stay in bounds whatever
+    the batch holds; flags that a malformed query_start_loc or block table
+    makes meaningless are not read, as the checks before them raise."""
+    n = len(batch.request_ids)
+    num_tokens = batch.input_token_ids.numel()
+    if num_tokens == 0 or width == 0:  # the checks before these raise
+        return torch.zeros(6, dtype=torch.bool, device=device)
+    qsl, ctx, tables = batch.query_start_loc, batch.context_lens, batch.block_tables
+    positions, slots = batch.positions, batch.slot_mapping
+    decoding = _upload([ph is RequestStatus.DECODING for ph in batch.request_phases],
+                       device).bool()
+    tokens = torch.arange(num_tokens, device=device)
+    owner = torch.searchsorted(qsl[1:].contiguous(), tokens, right=True).clamp_(max=n - 1)
+    lens = qsl[1:] - qsl[:-1]
+    expected_pos = (ctx - lens)[owner] + tokens - qsl[:-1][owner]
+    col = (positions // bs).clamp(0, width - 1)
+    expected_slot = tables[owner, col] * bs + positions % bs
+    dec = decoding[owner]
+    bad_pos = positions != expected_pos
+    bad_slot = slots != expected_slot
+    # Repeated slots within a phase: the phase in the key's low bit.
+    ordered = (slots * 2 + dec.long()).sort().values
+    repeat = ordered[1:] == ordered[:-1]
+    repeat_dec = (ordered[1:] & 1).bool()
+    return torch.stack([(bad_pos & ~dec).any(), (bad_slot & ~dec).any(),
+                        (repeat & ~repeat_dec).any(), (bad_pos & dec).any(),
+                        (bad_slot & dec).any(), (repeat & repeat_dec).any()])
 
 
 def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
@@ -338,14 +405,9 @@ def execute_model_batch(model, batch: ModelBatch, kv_cache: PagedKVCache,
                     block_tables=batch.block_tables.index_select(0, req),
                     context_lens=batch.context_lens.index_select(0, req))
 
-    # The metadata checks of both forwards (one host sync each) before either
-    # is queued; the forwards then skip them.
-    if packed is not None:
-        model.model.check_prefill_packed_inputs(*packed[:2], kv_cache, *packed[2:], max(lens))
-    if step is not None:
-        Qwen2Attention._check_decode_metadata(kv_cache, step["position_ids"],
-                                              step["slot_mapping"], step["block_tables"],
-                                              step["context_lens"])
+    # _check_batch ran both forwards' metadata checks; the cache's shape
+    # against the model is the one check of theirs left.
+    model.model._check_cache(kv_cache)
 
     # Each forward's LM head writes its rows of `logits` directly where they
     # are contiguous (the prefills lead in build_model_batch's order and the

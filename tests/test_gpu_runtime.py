@@ -344,3 +344,44 @@ def test_model_decode_rejects_bad_metadata_before_any_layer_writes(device):
             model.model.forward_decode_batch_with_cache(kv_cache=cache, **inputs)
     torch.cuda.synchronize()
     assert torch.equal(cache.k_cache, k0) and torch.equal(cache.v_cache, v0)
+
+
+@pytest.mark.parametrize("bad", ["prefill_position", "prefill_slot", "decode_slot",
+                                 "decode_duplicate"])
+def test_runner_rejects_bad_step_metadata_before_any_write(device, bad):
+    """execute_model_batch runs the packed prefill's and the batched decode's
+    metadata checks in its own single pass, before either forward: a bad
+    position or slot in either part of a step raises with that forward's
+    message, and nothing is written to the cache."""
+    from mini_llm_runtime_amd.runtime.model_runner import ModelBatch
+
+    model, cache, dec = _model_decode_case(device)
+    k0, v0 = cache.k_cache.clone(), cache.v_cache.clone()
+    t = lambda v: torch.tensor(v, dtype=torch.long, device=device)  # noqa: E731
+    # A three-token prompt in block 12, then the two decodes of the case.
+    slots = [12 * 4, 12 * 4 + 1, 12 * 4 + 2] + dec["slot_mapping"].tolist()
+    positions = [0, 1, 2] + dec["position_ids"][:, 0].tolist()
+    if bad == "prefill_position":
+        positions[1] = 2
+    elif bad == "prefill_slot":
+        slots[2] += 1
+    elif bad == "decode_slot":
+        slots[4] += 1
+    tables = [[12, -1, -1]] + dec["block_tables"].tolist()
+    ctx = [3] + dec["context_lens"].tolist()
+    if bad == "decode_duplicate":  # both decodes at context 5 of one table
+        tables[2], ctx[2], positions[4], slots[4] = tables[1], 5, 4, slots[3]
+    batch = ModelBatch(
+        request_ids=["p", "d0", "d1"], input_token_ids=t([5, 6, 7, 11, 42]),
+        positions=t(positions), query_start_loc=t([0, 3, 4, 5]),
+        request_phases=[RequestStatus.PREFILLING, RequestStatus.DECODING,
+                        RequestStatus.DECODING],
+        context_lens=t(ctx), block_tables=t(tables), slot_mapping=t(slots))
+    message = {"prefill_position": "position_ids must run from",
+               "prefill_slot": "slot_mapping must match", "decode_slot": "slot_mapping must match",
+               "decode_duplicate": "decode requests must use distinct write slots"}[bad]
+    with pytest.raises(ValueError, match=message):
+        with torch.no_grad():
+            execute_model_batch(model, batch, cache)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k_cache, k0) and torch.equal(cache.v_cache, v0)

@@ -230,6 +230,26 @@ def good_batch(**changes):
      "Decode requires exactly one token per request"),
     (dict(request_phases=[RequestStatus.PREFILLING, RequestStatus.WAITING]),
      "Unsupported request phase"),
+    # The packed prefill's and the batched decode's metadata checks, run in
+    # the same pass (model/qwen2.py check_prefill_packed_inputs,
+    # qwen2_attention.py _check_decode_metadata).
+    (dict(context_lens=torch.tensor([1, 5])), "context_lens must cover each request's tokens"),
+    (dict(positions=torch.tensor([0, 2, 4])), "position_ids must run from context_len"),
+    (dict(slot_mapping=torch.tensor([0, 2, 8])),
+     "slot_mapping must match block_tables and positions"),
+    (dict(positions=torch.tensor([0, 1, 3])), "decode positions must equal context_lens - 1"),
+    (dict(slot_mapping=torch.tensor([0, 1, 9])),
+     "slot_mapping must match block_tables and positions"),
+    (dict(request_phases=[RequestStatus.PREFILLING, RequestStatus.PREFILLING],
+          input_token_ids=torch.tensor([1, 2]), positions=torch.tensor([0, 0]),
+          query_start_loc=torch.tensor([0, 1, 2]), context_lens=torch.tensor([1, 1]),
+          block_tables=torch.tensor([[0], [0]]), slot_mapping=torch.tensor([0, 0])),
+     "packed tokens must use distinct write slots"),
+    (dict(request_phases=[RequestStatus.DECODING, RequestStatus.DECODING],
+          input_token_ids=torch.tensor([1, 2]), positions=torch.tensor([0, 0]),
+          query_start_loc=torch.tensor([0, 1, 2]), context_lens=torch.tensor([1, 1]),
+          block_tables=torch.tensor([[0], [0]]), slot_mapping=torch.tensor([0, 0])),
+     "decode requests must use distinct write slots"),
 ])
 def test_execute_model_batch_rejects(tiny_cpu, changes, message):
     model, cache = tiny_cpu
