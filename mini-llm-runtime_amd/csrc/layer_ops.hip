@@ -23,9 +23,14 @@
 //
 // One wave per row, four rows per 256-thread workgroup; 16-byte chunks when
 // the row length and every row start allow it, single elements otherwise.
-// The second pass re-reads the row (from residual_out when the add was fused)
-// from the caches. Both kernels are latency-bound at serving sizes (a few
-// rows of 896 elements) and bandwidth-bound at prefill sizes.
+// Rows of at most 256 chunks (2,048 16-bit or 1,024 FP32 elements) stay in
+// registers: every chunk of x, the residual and the weight is loaded before
+// anything is stored, so a wave makes one memory round trip before its
+// reduction instead of three (the loads, the re-read of the summed row, the
+// weight). Longer rows loop over their chunks and the second pass re-reads
+// the row (from residual_out when the add was fused) from the caches. Both
+// kernels are latency-bound at serving sizes (a few rows of 896 elements)
+// and bandwidth-bound at prefill sizes.
 #include <algorithm>
 #include <type_traits>
 
@@ -108,6 +113,79 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   }
 }
 
+// Rows of at most kWave * K chunks of N elements, held in registers (see the
+// file comment). Each lane adds its chunks and their elements in the order
+// rms_norm_kernel does, so the two kernels give the same bits.
+template <typename T, int N, int K>
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(
+    const T *x, int64_t x_stride, const T *residual, int64_t res_stride,
+    T *residual_out, int64_t res_out_stride, const T *__restrict__ weight, T *out,
+    int64_t out_stride, int64_t rows, int hidden, float factor, float eps) {
+  using E = Elem<T>;
+  using C = Chunk<T, N>;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves
+  const int chunks = hidden / N;
+  const C *xr = reinterpret_cast<const C *>(x + row * x_stride);
+  const C *wr = reinterpret_cast<const C *>(weight);
+  C r[K], w[K], b[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = lane + kWave * k;
+    if (c < chunks) {
+      r[k] = xr[c];
+      w[k] = wr[c];
+    }
+  }
+  if (residual != nullptr) {
+    const C *rr = reinterpret_cast<const C *>(residual + row * res_stride);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (lane + kWave * k < chunks) b[k] = rr[lane + kWave * k];
+    C *ro = reinterpret_cast<C *>(residual_out + row * res_out_stride);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = lane + kWave * k;
+      if (c < chunks) {
+#pragma unroll
+        for (int e = 0; e < N; ++e)
+          r[k].v[e] = E::from_f32(E::to_f32(b[k].v[e]) + E::to_f32(r[k].v[e]));
+        ro[c] = r[k];
+      }
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (lane + kWave * k < chunks) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float f = E::to_f32(r[k].v[e]);
+        sum += f * f;
+      }
+    }
+  sum = wave_sum(sum);
+  const float inv = rsqrtf(sum * factor + eps);
+  C *dst = reinterpret_cast<C *>(out + row * out_stride);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = lane + kWave * k;
+    if (c < chunks) {
+      C o;
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        float p = E::to_f32(r[k].v[e]) * inv;
+        // The FP32 rounding of the product stays, as in rms_norm_kernel.
+        if constexpr (std::is_same<T, f16_t>::value) asm volatile("" : "+v"(p));
+        const T n = E::from_f32(p);
+        o.v[e] = E::from_f32(E::to_f32(w[k].v[e]) * E::to_f32(n));
+      }
+      dst[c] = o;
+    }
+  }
+}
+
 template <typename T, int N>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const T *__restrict__ gate_up,
                                                        int64_t gu_stride, T *__restrict__ out,
@@ -152,9 +230,20 @@ int launch_norm(const void *x, int64_t xs, const void *res, int64_t rs, void *ro
   auto *rot = static_cast<T *>(ro);
   const auto *wt = static_cast<const T *>(w);
   auto *ot = static_cast<T *>(out);
-  if (vec)
+  const int h = static_cast<int>(hidden);
+  const int64_t chunks = hidden / N;
+  if (vec && chunks <= kWave)
+    rms_norm_rows_kernel<T, N, 1><<<blocks, 256, 0, stream>>>(xt, xs, rt, rs, rot, ros, wt, ot,
+                                                             os, rows, h, factor, eps);
+  else if (vec && chunks <= 2 * kWave)
+    rms_norm_rows_kernel<T, N, 2><<<blocks, 256, 0, stream>>>(xt, xs, rt, rs, rot, ros, wt, ot,
+                                                             os, rows, h, factor, eps);
+  else if (vec && chunks <= 4 * kWave)
+    rms_norm_rows_kernel<T, N, 4><<<blocks, 256, 0, stream>>>(xt, xs, rt, rs, rot, ros, wt, ot,
+                                                             os, rows, h, factor, eps);
+  else if (vec)
     rms_norm_kernel<T, N><<<blocks, 256, 0, stream>>>(xt, xs, rt, rs, rot, ros, wt, ot, os, rows,
-                                                     static_cast<int>(hidden), factor, eps);
+                                                     h, factor, eps);
   else
     rms_norm_kernel<T, 1><<<blocks, 256, 0, stream>>>(xt, xs, rt, rs, rot, ros, wt, ot, os, rows,
                                                      static_cast<int>(hidden), factor, eps);
