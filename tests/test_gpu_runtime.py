@@ -385,3 +385,53 @@ def test_runner_rejects_bad_step_metadata_before_any_write(device, bad):
             execute_model_batch(model, batch, cache)
     torch.cuda.synchronize()
     assert torch.equal(cache.k_cache, k0) and torch.equal(cache.v_cache, v0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_interleaved_phases_equal_the_grouped_batch(device, dtype):
+    """A step whose decodes and prefills alternate in the batch (so neither
+    part's logits rows are one range, and the runner gathers and scatters
+    them) gives, row for row, the logits and cache writes of the same
+    requests grouped prefills first (where each forward's LM head writes its
+    rows in place)."""
+    from mini_llm_runtime_amd.runtime.model_runner import ModelBatch
+
+    _, model, _ = make_model(TINY, dtype, device, seed=5)
+    t = lambda v: torch.tensor(v, dtype=torch.long, device=device)  # noqa: E731
+    P, D = RequestStatus.PREFILLING, RequestStatus.DECODING
+    # (phase, tokens, first position, block table) per request.
+    reqs = {"d0": (D, [11], 8, [0, 1, 2]), "p0": (P, [1, 2, 3, 4, 5], 0, [3, 4, -1]),
+            "d1": (D, [12], 5, [5, 6, -1]), "p1": (P, [7, 8, 9], 0, [7, -1, -1])}
+
+    def batch(order):
+        ids, pos, slots, qsl, ctx, tables = [], [], [], [0], [], []
+        for rid in order:
+            _, toks, start, table = reqs[rid]
+            for j in range(len(toks)):
+                p = start + j
+                ids.append(toks[j])
+                pos.append(p)
+                slots.append(table[p // 4] * 4 + p % 4)
+            qsl.append(qsl[-1] + len(toks))
+            ctx.append(start + len(toks))
+            tables.append(table)
+        return ModelBatch(request_ids=list(order), input_token_ids=t(ids), positions=t(pos),
+                          query_start_loc=t(qsl), request_phases=[reqs[r][0] for r in order],
+                          context_lens=t(ctx), block_tables=t(tables), slot_mapping=t(slots))
+
+    caches = []
+    for _ in range(2):
+        cache = PagedKVCache(2, 32, 4, 2, 16, dtype=dtype, device=device)
+        gen = torch.Generator().manual_seed(9)
+        cache.k_cache.copy_(torch.randn(cache.k_cache.shape, generator=gen).to(dtype))
+        cache.v_cache.copy_(torch.randn(cache.v_cache.shape, generator=gen).to(dtype))
+        caches.append(cache)
+    with torch.no_grad():
+        mixed = execute_model_batch(model, batch(["d0", "p0", "d1", "p1"]), caches[0])
+        grouped = execute_model_batch(model, batch(["p0", "p1", "d0", "d1"]), caches[1])
+    # Rows: mixed d0 | p0 x5 | d1 | p1 x3; grouped p0 x5 | p1 x3 | d0 | d1.
+    assert torch.equal(mixed[1:6], grouped[0:5])
+    assert torch.equal(mixed[7:10], grouped[5:8])
+    assert torch.equal(mixed[0], grouped[8]) and torch.equal(mixed[6], grouped[9])
+    assert torch.equal(caches[0].k_cache, caches[1].k_cache)
+    assert torch.equal(caches[0].v_cache, caches[1].v_cache)
